@@ -1,0 +1,202 @@
+"""Benchmark of the MLX affine quantized linear on one MI355X.
+
+Headline (``value``): 4-bit qmv at M=1, K=5120, N=17408, group 64 -- the
+north-star decode matvec -- in GB/s of algorithmic bytes (packed W + scales +
+biases + x + y, once each: 50,180,096 B per call) over whole-job time.  A
+step is one quantized_matmul call on one of 8 distinct weight sets used in
+rotation (8 x 50.2 MB = 401 MB > the 256 MB Infinity Cache), so weights
+stream from HBM.  Inputs are resident in HBM before the timed region; the K
+timed steps are replayed from a HIP graph so host launch overhead is not
+timed.  The qmm figure (M=2048, TFLOP/s of 2*M*N*K) is reported beside it.
+
+``cpu_baseline`` times the CPU oracle's fused dequant-dot (the reference's
+dequantize-then-matmul arithmetic, oracle/lisaq_oracle.c) on the host cores
+over a bounded number of calls of the same shape.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "4-bit qmv GB/s (% HBM peak) @M=1; qmm TFLOP/s (% bf16 MFMA peak) @M=2048"
+
+
+def qmv_bytes(M, N, K, bits=4, gs=64):
+    return N * K * bits // 8 + 2 * 2 * N * (K // gs) + 2 * M * K + 2 * M * N
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--qmm-steps", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from lisa_amd import ops
+    from lisa_amd.synth import torch_linear, torch_x
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x5EED + 1)
+    M, N, K, bits, gs = 1, 17408, 5120, 4, 64
+
+    # --- qmv: cold-stream rotation over distinct weight sets ------------------
+    sets = [torch_linear(N, K, bits, gs, device=dev, generator=gen) for _ in range(args.sets)]
+    x = torch_x(M, K, device=dev, generator=gen)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def step(i):
+        w, s, b = sets[i % len(sets)]
+        return ops.quantized_matmul(x, w, s, b, True, gs, bits)
+
+    with torch.cuda.stream(stream):
+        for i in range(max(args.warmup, len(sets))):  # eager warmup (also allocates the workspace)
+            step(i)
+    stream.synchronize()
+
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(n):
+                step(i)
+        return g
+
+    g_warm = capture(len(sets))
+    g_timed = capture(args.steps)
+    with torch.cuda.stream(stream):
+        g_warm.replay()
+    torch.cuda.synchronize()
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        g_timed.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    per_step_s = gpu_ms * 1e-3 / args.steps
+    nbytes = qmv_bytes(M, N, K, bits, gs)
+    gbs = nbytes / per_step_s / 1e9
+
+    # --- qmm: prefill M=2048 (eager; each call is ~0.3-1 ms) -------------------
+    Mq = 2048
+    wq = sets[0]
+    xq = torch_x(Mq, K, device=dev, generator=gen)
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            ops.quantized_matmul(xq, *wq, True, gs, bits)
+    torch.cuda.synchronize()
+    q0 = torch.cuda.Event(enable_timing=True)
+    q1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        q0.record(stream)
+        for _ in range(args.qmm_steps):
+            ops.quantized_matmul(xq, *wq, True, gs, bits)
+        q1.record(stream)
+    torch.cuda.synchronize()
+    qmm_s = q0.elapsed_time(q1) * 1e-3 / args.qmm_steps
+    flops = 2.0 * Mq * N * K
+    tflops = flops / qmm_s / 1e12
+
+    # --- CPU baseline (oracle fused dequant-dot, same shape, bounded sample) ---
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(M, N, K, bits, gs, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(per_step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "qmv 4-bit gs64 M=1 K=5120 N=17408 (decode matvec), 8 rotating weight sets",
+            "bits": bits, "group_size": gs, "M": M, "K": K, "N": N, "weight_sets": len(sets),
+            "bytes_per_step": nbytes, "timing": "HIP graph replay of the timed steps, hipEvent bracket",
+            "wall_s": round(wall, 4),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "lisaq::qmv_kernel<4,64,1,4>", "bytes_per_launch": nbytes,
+            "avg_launch_us": round(per_step_s * 1e6, 3),
+        },
+        "qmm": {
+            "workload": "qmm 4-bit gs64 M=2048 K=5120 N=17408 (prefill)",
+            "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_call": round(qmm_s * 1e3, 4),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(M, N, K, bits, gs, seconds):
+    """Oracle fused dequant-dot on host threads over a bounded number of calls."""
+    import numpy as np
+
+    from lisa_amd.synth import np_linear, np_x
+    from oracle import oracle as O
+
+    O.build()
+    rng = np.random.default_rng(0x5EED)
+    w, s, b = np_linear(rng, N, K, bits, gs)
+    x = np_x(rng, M, K)
+    threads = min(16, os.cpu_count() or 1)
+    res = {}
+    for nt in (threads, 1):
+        budget = seconds * (0.75 if nt == threads else 0.25)
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            O.qmv_threads(x, w, s, b, gs, bits, nt)
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                break
+        res[nt] = (calls, el)
+    calls, el = res[threads]
+    nbytes = qmv_bytes(M, N, K, bits, gs)
+    c1, e1 = res[1]
+    return {
+        "value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"{calls} calls of the same qmv shape (M=1 K=5120 N=17408 4-bit) in {el:.1f} s on {threads} "
+                  f"threads; 1 thread: {nbytes * c1 / e1 / 1e9:.3f} GB/s ({c1} calls)",
+        "us_per_call": round(el / calls * 1e6, 1),
+    }
+
+
+if __name__ == "__main__":
+    main()

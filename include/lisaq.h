@@ -1,0 +1,191 @@
+/*
+ * lisaq.h -- C ABI of liblisaq, the MI355X (gfx950) implementation of LISA's
+ * MLX-format affine group-quantized linear layer.
+ *
+ * Packed layout (identical to MLX / LISA safetensors):
+ *   w       uint32 [N, K*bits/32]  codes little-end-first along K:
+ *           code(n,k) = (w[n, k/(32/bits)] >> (bits*(k%(32/bits)))) & (2^bits-1)
+ *   scales  bf16   [N, K/group_size]
+ *   biases  bf16   [N, K/group_size]
+ *   value   w(n,k) = scales[n, k/gs] * code(n,k) + biases[n, k/gs]
+ *
+ * Conventions for every entry point:
+ *   - all tensor pointers are DEVICE pointers, row-major and contiguous;
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream); calls are
+ *     stream-ordered, return right after enqueue and never synchronize;
+ *   - the caller owns every buffer, including outputs and workspaces; no entry
+ *     point allocates device memory;
+ *   - return value is a lisaq_status; on failure lisaq_last_error() holds a
+ *     message for the calling thread and nothing was enqueued.
+ *
+ * Reference paths below are relative to the agnosticeng/lisa checkout
+ * (AO = crates/lisa-mlx/src/ops/array_ops.rs, EQ = crates/lisa-engine/src/
+ * core/quant.rs, EM = crates/lisa-engine/src/models/qwen4/moe.rs,
+ * KM = crates/lisa-mlx/src/models/qwen4/kernels/moe.rs).
+ */
+#ifndef LISAQ_H
+#define LISAQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define LISAQ_API __attribute__((visibility("default")))
+#else
+#define LISAQ_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  LISAQ_OK = 0,
+  LISAQ_EINVAL_SHAPE = 1,   /* inconsistent or unsupported sizes            */
+  LISAQ_EINVAL_DTYPE = 2,   /* dtype not supported by this entry point      */
+  LISAQ_EINVAL_LAYOUT = 3,  /* null/misaligned pointer, transpose=false ... */
+  LISAQ_EUNSUPPORTED = 4,   /* bits/group_size/path not implemented         */
+  LISAQ_EHIP = 5,           /* the HIP runtime reported an error            */
+  LISAQ_EWORKSPACE = 6      /* workspace missing or too small               */
+} lisaq_status;
+
+typedef enum { LISAQ_DTYPE_BF16 = 0, LISAQ_DTYPE_F32 = 1 } lisaq_dtype;
+
+/* Library version (major*10000 + minor*100 + patch). */
+LISAQ_API int lisaq_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+LISAQ_API const char* lisaq_last_error(void);
+
+/* ---- quantized matmul ---------------------------------------------------
+ * y[M,N] (bf16) = x[M,K] (bf16) . dequant(w)^T.
+ * Replaces ops::quantized_matmul (AO:378-493).  transpose must be 1 and
+ * biases non-NULL (AO:387-392).  Dispatch follows the reference: M <
+ * qmv_batch_limit(K,N) takes the matvec path (f32 weights, per-group
+ * scale*sum(x*q) + bias*sum(x), AO:405-470), larger M the matmul path
+ * (weights rounded to bf16 in the tile, f32 accumulate, AO:471-489).
+ * workspace: lisaq_quantized_matmul_workspace() bytes (also enough for
+ * lisaq_qmv at the same M), 256-byte aligned.  Its first 128 KiB hold
+ * split-K arrival counters: they must be zero before the first use, every
+ * call leaves them zero, and no other entry point may write them (give
+ * gather_qmm / moe_forward their own workspace).  Calls that share a
+ * workspace must be ordered on one stream.  serial_rows with M rows needs
+ * 128 KiB + M * (size(M=1) - 128 KiB) bytes. */
+LISAQ_API int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, void* y, int64_t M, int64_t N, int64_t K,
+                           int transpose, int group_size, int bits, void* workspace,
+                           size_t workspace_bytes);
+LISAQ_API size_t lisaq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_size, int bits);
+
+/* Replaces ops::quantized_matmul_serial_rows (AO:500-555): each of the M<=8
+ * rows gets the same arithmetic as an independent M=1 call (bitwise), and
+ * M outside 2..8 falls back to lisaq_quantized_matmul. */
+LISAQ_API int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32_t* w,
+                                       const void* scales, const void* biases, void* y, int64_t M,
+                                       int64_t N, int64_t K, int transpose, int group_size,
+                                       int bits, void* workspace, size_t workspace_bytes);
+
+/* Forced paths (no dispatch), same arguments.  qmv accepts 1 <= M <= 32
+ * (jit::affine_qmv_fast JM:186-302, jit::qmv_wide JM:1799-1869); qmm any M
+ * (jit::affine_qmm JM:1984-2055). */
+LISAQ_API int lisaq_qmv(void* stream, const void* x, const uint32_t* w, const void* scales,
+              const void* biases, void* y, int64_t M, int64_t N, int64_t K, int group_size,
+              int bits, void* workspace, size_t workspace_bytes);
+LISAQ_API int lisaq_qmm(void* stream, const void* x, const uint32_t* w, const void* scales,
+              const void* biases, void* y, int64_t M, int64_t N, int64_t K, int group_size,
+              int bits, void* workspace, size_t workspace_bytes);
+
+/* ---- dequantize / quantize ----------------------------------------------
+ * out[rows,K] (bf16) = scales*code + biases.  Replaces ops::dequantize
+ * (AO:37-84; GPU kernel jit::affine_dequantize JM:1316-1402). */
+LISAQ_API int lisaq_dequantize(void* stream, const uint32_t* w, const void* scales, const void* biases,
+                     void* out, int64_t rows, int64_t K, int group_size, int bits);
+
+/* Replaces ops::quantize (AO:218-290).  w is [rows,K] of `dtype` (bf16 or
+ * f32); scales/biases are written in the same dtype, wq as uint32
+ * [rows, K*bits/32].  Requires K % gs == 0 and gs % (32/bits) == 0. */
+LISAQ_API int lisaq_quantize(void* stream, const void* w, int dtype, uint32_t* wq, void* scales,
+                   void* biases, int64_t rows, int64_t K, int group_size, int bits);
+
+/* ---- MoE (generic SparseMoeBlock path, EM:335-483) ----------------------
+ * Router: logits f32 [T,E] -> top-k expert ids (descending logit, ties to the
+ * lower id, as the stable argsort of -logits, EM:355-357) and f32 weights
+ * = softmax over the k selected logits (EM:358-359).  1 <= k <= 32, E <= 1024. */
+LISAQ_API int lisaq_moe_route(void* stream, const float* logits, int64_t T, int E, int k, int32_t* topk_idx,
+                    float* topk_weights);
+
+/* Gather permutation of the R = T*k routed slots (EM:364-374, KM:132-242):
+ *   order       = stable argsort of idx_flat     (slot index per sorted row)
+ *   sorted_idx  = idx_flat[order]                (expert id per sorted row)
+ *   token_rows  = order / top_k                  (token per sorted row)
+ *   inverse     = argsort(order)                 (sorted row per slot)
+ *   expert_offsets[E+1]: first sorted row of each expert, [E] = R.
+ * Bit-exact; ids outside [0,E) fail with LISAQ_EINVAL_SHAPE (checked on the
+ * device: the call then writes expert_offsets[E] = -1).  R <= 2^24. */
+LISAQ_API int lisaq_moe_sort(void* stream, const int32_t* idx_flat, int64_t R, int E, int top_k,
+                   int32_t* sorted_idx, int32_t* order, int32_t* token_rows, int32_t* inverse,
+                   int32_t* expert_offsets);
+
+/* out[r,:] = x[rows[r],:] for bf16 rows of length H (x_sorted, EM:372). */
+LISAQ_API int lisaq_gather_rows(void* stream, const void* x, const int32_t* rows, void* out, int64_t R,
+                      int64_t H);
+
+/* gather_qmm (AO:561-642): x [R,K] bf16 rows sorted by expert; w [E,N,K*bits/32],
+ * scales/biases [E,N,K/gs]; rhs_indices int32 [R] (sorted: each contiguous
+ * run of one expert id is one matmul); y [R,N] bf16.  Each run uses the
+ * arithmetic quantized_matmul would use for a run of that length (matvec
+ * below qmv_batch_limit, matmul above), as the reference's per-run loop
+ * (AO:591-630) does.  workspace: lisaq_gather_qmm_workspace() bytes. */
+LISAQ_API int lisaq_gather_qmm(void* stream, const void* x, const uint32_t* w, const void* scales,
+                     const void* biases, const int32_t* rhs_indices, void* y, int64_t R,
+                     int64_t N, int64_t K, int E, int transpose, int group_size, int bits,
+                     void* workspace, size_t workspace_bytes);
+LISAQ_API size_t lisaq_gather_qmm_workspace(int64_t R, int64_t N, int64_t K, int E, int group_size,
+                                  int bits);
+
+/* act = bf16(silu(gate)) * up in bf16 (EM:413, core/norm.rs bf16_silu). */
+LISAQ_API int lisaq_swiglu(void* stream, const void* gate, const void* up, void* act, int64_t n);
+
+/* Sorted combine (KM:38-119, moe_combine.metal): out[t,d] (bf16) =
+ * bf16( colsum_small<k>( f32(down_sorted[inverse[t*k+j], d]) * w[t*k+j] ) ).
+ * Bit-exact with the reference summation order.  1 <= k <= 32. */
+LISAQ_API int lisaq_moe_combine(void* stream, const void* down_sorted, const float* weights,
+                      const int32_t* inverse, void* out, int64_t T, int k, int64_t H);
+
+/* The whole routed SwitchGLU of SparseMoeBlock::forward's generic path
+ * (EM:352-449): route -> sort -> gather -> gate/up gather_qmm -> SwiGLU ->
+ * down gather_qmm -> combine.  x [T,H] bf16, logits f32 [T,E]; expert stacks
+ * gate/up [E,I,H*bits/32] (+ scales/biases [E,I,H/gs]) and down
+ * [E,H,I*bits/32] (+ [E,H,I/gs]); out [T,H] bf16.  Optional outputs
+ * topk_idx/topk_weights [T,k] may be NULL.
+ * workspace: lisaq_moe_workspace() bytes, zero-filled before first use. */
+LISAQ_API int lisaq_moe_forward(void* stream, const void* x, const float* logits, const uint32_t* gate_w,
+                      const void* gate_s, const void* gate_b, const uint32_t* up_w,
+                      const void* up_s, const void* up_b, const uint32_t* down_w,
+                      const void* down_s, const void* down_b, void* out, int64_t T, int64_t H,
+                      int64_t I, int E, int k, int group_size, int bits, int32_t* topk_idx,
+                      float* topk_weights, void* workspace, size_t workspace_bytes);
+LISAQ_API size_t lisaq_moe_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int group_size,
+                           int bits);
+
+/* ---- layout helpers (host only, no device work) -------------------------
+ * detect_group_size (EQ:273-287): gs = (weight_cols*32/bits)/scales_cols when
+ * that divides exactly and 1 <= gs <= 4096, else -1. */
+LISAQ_API int lisaq_detect_group_size(int64_t weight_cols, int64_t scales_cols, int bits);
+
+/* qmv_batch_limit (jit/matmul.rs:1873-1881): 33 if K,N <= 2048; 25 if
+ * K,N <= 4096; else 13. */
+LISAQ_API int lisaq_qmv_batch_limit(int64_t K, int64_t N);
+
+/* Validates the packed triple of one quantized linear (shapes as given by
+ * the safetensors header, EQ:408-428 + LD:57-150): w [N, Kq] u32, scales and
+ * biases [N, G].  Writes K and the detected group size.  LISAQ_OK or
+ * LISAQ_EINVAL_SHAPE with a message. */
+LISAQ_API int lisaq_check_layout(int64_t w_rows, int64_t w_cols, int64_t s_rows, int64_t s_cols,
+                       int64_t b_rows, int64_t b_cols, int bits, int64_t* K_out,
+                       int* group_size_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LISAQ_H */

@@ -1,0 +1,460 @@
+// C ABI of liblisaq: validation, dispatch and workspace layout.
+//
+// Mirrors the reference op surface (crates/lisa-mlx/src/ops/array_ops.rs):
+// the same preconditions are checked and reported as status codes instead of
+// Err(String), and the same shape-based dispatch picks the kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kernels.h"
+#include "lisaq_common.h"
+#include "qmm.h"
+#include "qmv.h"
+
+namespace lisaq {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(LISAQ_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return LISAQ_OK;
+}
+
+static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Shared validation of one quantized matmul problem (array_ops.rs:387-404,
+// :227-229; jit/matmul.rs:270-277).
+static int validate_mm(const char* op, const void* x, const uint32_t* w, const void* s, const void* b,
+                       const void* y, int64_t M, int64_t N, int64_t K, int transpose, int gs, int bits) {
+  LISAQ_REQUIRE(transpose == 1, LISAQ_EINVAL_LAYOUT, "%s: only transpose=true supported", op);
+  LISAQ_REQUIRE(b != nullptr, LISAQ_EINVAL_LAYOUT, "%s: affine biases required", op);
+  LISAQ_REQUIRE(M >= 0 && N >= 0 && K >= 0, LISAQ_EINVAL_SHAPE, "%s: negative size", op);
+  LISAQ_REQUIRE(bits == 2 || bits == 4, LISAQ_EUNSUPPORTED, "%s: bits=%d not supported (2 or 4)", op, bits);
+  LISAQ_REQUIRE(gs == 32 || gs == 64 || gs == 128, LISAQ_EUNSUPPORTED,
+                "%s: group_size=%d not supported (32, 64 or 128)", op, gs);
+  LISAQ_REQUIRE(K % gs == 0 && gs % (32 / bits) == 0, LISAQ_EINVAL_SHAPE,
+                "%s: group size %d incompatible with K=%lld, bits=%d", op, gs, (long long)K, bits);
+  LISAQ_REQUIRE(M <= (int64_t)1 << 31 && N <= (int64_t)1 << 31 && K <= (int64_t)1 << 30, LISAQ_EINVAL_SHAPE,
+                "%s: size too large", op);
+  if (M == 0 || N == 0 || K == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(x && w && s && y, LISAQ_EINVAL_LAYOUT, "%s: null tensor pointer", op);
+  LISAQ_REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(y, 4), LISAQ_EINVAL_LAYOUT,
+                "%s: x and w must be 16-byte aligned, y 4-byte aligned", op);
+  LISAQ_REQUIRE(aligned(s, 8) && aligned(b, 8), LISAQ_EINVAL_LAYOUT, "%s: scales/biases must be 8-byte aligned",
+                op);
+  return LISAQ_OK;
+}
+
+static int run_qmv(hipStream_t st, const QmvConfig& c, const void* x, const uint32_t* w, const void* s,
+                   const void* b, void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, void* ws,
+                   size_t ws_bytes) {
+  if (c.S > 1) {
+    LISAQ_REQUIRE(ws != nullptr && ws_bytes >= c.ws_bytes, LISAQ_EWORKSPACE,
+                  "qmv: workspace of %zu bytes required (got %zu)", c.ws_bytes, ws_bytes);
+    LISAQ_REQUIRE(aligned(ws, 256), LISAQ_EINVAL_LAYOUT, "qmv: workspace must be 256-byte aligned");
+  }
+  QmvParams p{};
+  p.x = (const uint16_t*)x;
+  p.w = w;
+  p.s = (const uint16_t*)s;
+  p.b = (const uint16_t*)b;
+  p.y = (uint16_t*)y;
+  p.counters = (uint32_t*)ws;
+  p.partial = ws ? (float*)((char*)ws + kQmvCounterBytes) : nullptr;
+  p.tiles = nullptr;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.G = (int)(K / gs);
+  p.part_rows = (int)M;
+  return qmv_launch(st, c, p, bits, gs, c.tiles);
+}
+
+static int run_qmm(hipStream_t st, const void* x, const uint32_t* w, const void* s, const void* b, void* y,
+                   int64_t M, int64_t N, int64_t K, int gs, int bits) {
+  LISAQ_REQUIRE(K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm: K=%lld must be a multiple of 64", (long long)K);
+  const QmmConfig c = qmm_config(M, N, K, gs, bits);
+  QmmParams p{};
+  p.x = (const uint16_t*)x;
+  p.w = w;
+  p.s = (const uint16_t*)s;
+  p.b = (const uint16_t*)b;
+  p.y = (uint16_t*)y;
+  p.tiles = nullptr;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.G = (int)(K / gs);
+  return qmm_launch(st, c, p, bits, gs, c.grid_n, c.grid_m);
+}
+
+// Gather workspace layout: [counts 256 B][qmv table][qmm table], 256-B aligned.
+struct GatherLayout {
+  int limit, Mmax, qmv_cap, qmm_cap;
+  size_t qmv_off, qmm_off, total;
+  QmvConfig qc;
+  QmmConfig mc;
+};
+
+static size_t up256(size_t v) { return (v + 255) / 256 * 256; }
+
+static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs, int bits) {
+  GatherLayout L{};
+  L.limit = lisaq_qmv_batch_limit(K, N);
+  const int64_t runs = R < E ? R : E;
+  L.Mmax = (int)((R < L.limit - 1) ? R : L.limit - 1);
+  if (L.Mmax < 1) L.Mmax = 1;
+  L.qc = qmv_config(L.Mmax, N, K, gs, bits, /*single_pass=*/true);
+  L.mc = qmm_config(L.limit, N, K, gs, bits);
+  L.qmv_cap = (int)(runs * ((N + 31) / 32));
+  L.qmm_cap = (R >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
+  L.qmv_off = 256;
+  L.qmm_off = L.qmv_off + up256((size_t)L.qmv_cap * 16);
+  L.total = L.qmm_off + up256((size_t)L.qmm_cap * 16);
+  return L;
+}
+
+}  // namespace lisaq
+
+using namespace lisaq;
+
+extern "C" {
+
+int lisaq_version(void) { return 100; }
+
+const char* lisaq_last_error(void) { return g_err; }
+
+int lisaq_qmv_batch_limit(int64_t K, int64_t N) {
+  if (K <= 2048 && N <= 2048) return 33;
+  if (K <= 4096 && N <= 4096) return 25;
+  return 13;
+}
+
+int lisaq_detect_group_size(int64_t weight_cols, int64_t scales_cols, int bits) {
+  if (weight_cols <= 0 || scales_cols <= 0 || bits <= 0 || 32 % bits != 0) return -1;
+  const int64_t k = weight_cols * (32 / bits);
+  if (k > INT32_MAX) return -1;
+  if (k % scales_cols != 0) return -1;
+  const int64_t g = k / scales_cols;
+  return (g >= 1 && g <= 4096) ? (int)g : -1;
+}
+
+int lisaq_check_layout(int64_t w_rows, int64_t w_cols, int64_t s_rows, int64_t s_cols, int64_t b_rows,
+                       int64_t b_cols, int bits, int64_t* K_out, int* gs_out) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(bits > 0 && 32 % bits == 0, LISAQ_EINVAL_SHAPE, "check_layout: bits=%d invalid", bits);
+  LISAQ_REQUIRE(w_rows > 0 && w_cols > 0, LISAQ_EINVAL_SHAPE, "check_layout: empty weight");
+  LISAQ_REQUIRE(s_rows == w_rows && b_rows == w_rows, LISAQ_EINVAL_SHAPE,
+                "check_layout: scales/biases rows (%lld, %lld) != weight rows %lld", (long long)s_rows,
+                (long long)b_rows, (long long)w_rows);
+  LISAQ_REQUIRE(b_cols == s_cols, LISAQ_EINVAL_SHAPE, "check_layout: biases cols %lld != scales cols %lld",
+                (long long)b_cols, (long long)s_cols);
+  const int gs = lisaq_detect_group_size(w_cols, s_cols, bits);
+  LISAQ_REQUIRE(gs > 0, LISAQ_EINVAL_SHAPE, "check_layout: no group size fits weight cols %lld, scales cols %lld",
+                (long long)w_cols, (long long)s_cols);
+  LISAQ_REQUIRE(gs % (32 / bits) == 0, LISAQ_EINVAL_SHAPE, "check_layout: group size %d splits a u32 word", gs);
+  if (K_out) *K_out = w_cols * (32 / bits);
+  if (gs_out) *gs_out = gs;
+  return LISAQ_OK;
+}
+
+size_t lisaq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+  if (M <= 0 || N <= 0 || K <= 0 || gs <= 0 || K % gs) return 0;
+  if (M > 32) return 0;  // matmul path: no workspace
+  // covers both the dispatched path and the forced matvec path at this M
+  return qmv_config(M, N, K, gs, bits).ws_bytes;
+}
+
+int lisaq_qmv(void* stream, const void* x, const uint32_t* w, const void* s, const void* b, void* y,
+              int64_t M, int64_t N, int64_t K, int gs, int bits, void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  int rc = validate_mm("qmv", x, w, s, b, y, M, N, K, 1, gs, bits);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(M <= 32, LISAQ_EINVAL_SHAPE, "qmv: M=%lld > 32", (long long)M);
+  LISAQ_REQUIRE(K > 0, LISAQ_EINVAL_SHAPE, "qmv: K=0");
+  const QmvConfig c = qmv_config(M, N, K, gs, bits);
+  return run_qmv((hipStream_t)stream, c, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
+}
+
+int lisaq_qmm(void* stream, const void* x, const uint32_t* w, const void* s, const void* b, void* y,
+              int64_t M, int64_t N, int64_t K, int gs, int bits, void* ws, size_t ws_bytes) {
+  (void)ws;
+  (void)ws_bytes;
+  g_err[0] = 0;
+  int rc = validate_mm("qmm", x, w, s, b, y, M, N, K, 1, gs, bits);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(K > 0, LISAQ_EINVAL_SHAPE, "qmm: K=0");
+  return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits);
+}
+
+int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t* w, const void* s, const void* b,
+                           void* y, int64_t M, int64_t N, int64_t K, int transpose, int gs, int bits,
+                           void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  int rc = validate_mm("quantized_matmul", x, w, s, b, y, M, N, K, transpose, gs, bits);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(K > 0, LISAQ_EINVAL_SHAPE, "quantized_matmul: K=0");
+  if (M < lisaq_qmv_batch_limit(K, N)) {
+    const QmvConfig c = qmv_config(M, N, K, gs, bits);
+    return run_qmv((hipStream_t)stream, c, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
+  }
+  return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits);
+}
+
+int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32_t* w, const void* s,
+                                       const void* b, void* y, int64_t M, int64_t N, int64_t K, int transpose,
+                                       int gs, int bits, void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  int rc = validate_mm("quantized_matmul_serial_rows", x, w, s, b, y, M, N, K, transpose, gs, bits);
+  if (rc) return rc;
+  if (M <= 1 || M > 8)
+    return lisaq_quantized_matmul(stream, x, w, s, b, y, M, N, K, transpose, gs, bits, ws, ws_bytes);
+  // The M=1 schedule (same slabs, same waves) applied to every row gives each
+  // row the arithmetic of an independent M=1 call.
+  const QmvConfig c = qmv_config(1, N, K, gs, bits);
+  QmvConfig cm = c;
+  cm.lds_bytes = qmv_lds_bytes(c.slab_groups, gs, (int)M, 1, bits, c.NW);
+  cm.ws_bytes = c.S > 1 ? kQmvCounterBytes + (size_t)c.S * M * N * 4 : 0;
+  if (cm.lds_bytes <= 64 * 1024)
+    return run_qmv((hipStream_t)stream, cm, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
+  for (int64_t r = 0; r < M; ++r) {
+    rc = run_qmv((hipStream_t)stream, c, (const uint16_t*)x + r * K, w, s, b, (uint16_t*)y + r * N, 1, N, K, gs,
+                 bits, ws, ws_bytes);
+    if (rc) return rc;
+  }
+  return LISAQ_OK;
+}
+
+int lisaq_dequantize(void* stream, const uint32_t* w, const void* s, const void* b, void* out, int64_t rows,
+                     int64_t K, int gs, int bits) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(bits == 2 || bits == 4 || bits == 8, LISAQ_EUNSUPPORTED, "dequantize: bits=%d not supported",
+                bits);
+  LISAQ_REQUIRE(rows >= 0 && K >= 0 && gs > 0, LISAQ_EINVAL_SHAPE, "dequantize: bad sizes");
+  LISAQ_REQUIRE(K % gs == 0 && gs % (32 / bits) == 0, LISAQ_EINVAL_SHAPE,
+                "dequantize: group size %d incompatible with K=%lld, bits=%d", gs, (long long)K, bits);
+  if (rows == 0 || K == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(w && s && b && out, LISAQ_EINVAL_LAYOUT, "dequantize: null tensor pointer");
+  LISAQ_REQUIRE(aligned(out, 16) && K % 8 == 0, LISAQ_EINVAL_LAYOUT,
+                "dequantize: out must be 16-byte aligned and K a multiple of 8");
+  return launch_dequantize((hipStream_t)stream, w, (const uint16_t*)s, (const uint16_t*)b, (uint16_t*)out, rows,
+                           K, gs, bits);
+}
+
+int lisaq_quantize(void* stream, const void* w, int dtype, uint32_t* wq, void* s, void* b, int64_t rows,
+                   int64_t K, int gs, int bits) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(dtype == LISAQ_DTYPE_BF16 || dtype == LISAQ_DTYPE_F32, LISAQ_EINVAL_DTYPE,
+                "quantize: dtype %d not supported", dtype);
+  LISAQ_REQUIRE(bits == 2 || bits == 4 || bits == 8, LISAQ_EUNSUPPORTED, "quantize: bits=%d not supported", bits);
+  LISAQ_REQUIRE(rows >= 0 && K >= 0 && gs > 0, LISAQ_EINVAL_SHAPE, "quantize: bad sizes");
+  LISAQ_REQUIRE(K % gs == 0 && gs % (32 / bits) == 0, LISAQ_EINVAL_SHAPE,
+                "quantize: group size %d incompatible with K=%lld, bits=%d", gs, (long long)K, bits);
+  if (rows == 0 || K == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(w && wq && s && b, LISAQ_EINVAL_LAYOUT, "quantize: null tensor pointer");
+  return launch_quantize((hipStream_t)stream, w, dtype, wq, s, b, rows, K, gs, bits);
+}
+
+int lisaq_moe_route(void* stream, const float* logits, int64_t T, int E, int k, int32_t* idx, float* wts) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(T >= 0 && E >= 1 && E <= 1024, LISAQ_EINVAL_SHAPE, "moe_route: need 1 <= E <= 1024 (E=%d)", E);
+  LISAQ_REQUIRE(k >= 1 && k <= 32 && k <= E, LISAQ_EINVAL_SHAPE, "moe_route: need 1 <= k <= min(32, E) (k=%d)", k);
+  if (T == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(logits && idx && wts, LISAQ_EINVAL_LAYOUT, "moe_route: null tensor pointer");
+  return launch_route((hipStream_t)stream, logits, T, E, k, idx, wts);
+}
+
+int lisaq_moe_sort(void* stream, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,
+                   int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(R >= 0 && R <= (1 << 24), LISAQ_EINVAL_SHAPE, "moe_sort: R=%lld out of range", (long long)R);
+  LISAQ_REQUIRE(E >= 1 && E <= 1024 && top_k >= 1, LISAQ_EINVAL_SHAPE, "moe_sort: need 1 <= E <= 1024, top_k >= 1");
+  LISAQ_REQUIRE(offsets, LISAQ_EINVAL_LAYOUT, "moe_sort: null offsets");
+  LISAQ_REQUIRE(R == 0 || (ids && sorted_idx && order && token_rows && inverse), LISAQ_EINVAL_LAYOUT,
+                "moe_sort: null tensor pointer");
+  return launch_sort((hipStream_t)stream, ids, R, E, top_k, sorted_idx, order, token_rows, inverse, offsets);
+}
+
+int lisaq_gather_rows(void* stream, const void* x, const int32_t* rows, void* out, int64_t R, int64_t H) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(R >= 0 && H >= 0, LISAQ_EINVAL_SHAPE, "gather_rows: negative size");
+  if (R == 0 || H == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(x && rows && out, LISAQ_EINVAL_LAYOUT, "gather_rows: null tensor pointer");
+  if (H % 8 == 0)
+    LISAQ_REQUIRE(aligned(x, 16) && aligned(out, 16), LISAQ_EINVAL_LAYOUT, "gather_rows: 16-byte alignment needed");
+  return launch_gather_rows((hipStream_t)stream, (const uint16_t*)x, rows, (uint16_t*)out, R, H);
+}
+
+size_t lisaq_gather_qmm_workspace(int64_t R, int64_t N, int64_t K, int E, int gs, int bits) {
+  if (R <= 0 || N <= 0 || K <= 0 || E <= 0 || gs <= 0 || K % gs) return 256;
+  return gather_layout(R, N, K, E, gs, bits).total;
+}
+
+int lisaq_gather_qmm(void* stream, const void* x, const uint32_t* w, const void* s, const void* b,
+                     const int32_t* rhs, void* y, int64_t R, int64_t N, int64_t K, int E, int transpose, int gs,
+                     int bits, void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  int rc = validate_mm("gather_qmm", x, w, s, b, y, R, N, K, transpose, gs, bits);
+  if (rc) return rc;
+  LISAQ_REQUIRE(E >= 1, LISAQ_EINVAL_SHAPE, "gather_qmm: E=%d", E);
+  if (R == 0 || N == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(K > 0, LISAQ_EINVAL_SHAPE, "gather_qmm: K=0");
+  LISAQ_REQUIRE(rhs != nullptr, LISAQ_EINVAL_LAYOUT, "gather_qmm: rhs_indices required");
+  LISAQ_REQUIRE(R <= (1 << 24), LISAQ_EINVAL_SHAPE, "gather_qmm: R=%lld too large", (long long)R);
+  const GatherLayout L = gather_layout(R, N, K, E, gs, bits);
+  LISAQ_REQUIRE(ws != nullptr && ws_bytes >= L.total && aligned(ws, 256), LISAQ_EWORKSPACE,
+                "gather_qmm: 256-byte aligned workspace of %zu bytes required (got %zu)", L.total, ws_bytes);
+  if (L.qmm_cap > 0)
+    LISAQ_REQUIRE(K % 64 == 0, LISAQ_EUNSUPPORTED, "gather_qmm: K=%lld must be a multiple of 64", (long long)K);
+  hipStream_t st = (hipStream_t)stream;
+  char* base = (char*)ws;
+  int32_t* counts = (int32_t*)base;
+  int4* qmv_tab = (int4*)(base + L.qmv_off);
+  int4* qmm_tab = (int4*)(base + L.qmm_off);
+  rc = launch_tile_table(st, rhs, R, (int)N, L.limit, L.mc.BM, L.mc.BN, qmv_tab, L.qmv_cap, qmm_tab, L.qmm_cap,
+                         counts);
+  if (rc) return rc;
+  if (L.qmv_cap > 0) {
+    QmvParams p{};
+    p.x = (const uint16_t*)x;
+    p.w = w;
+    p.s = (const uint16_t*)s;
+    p.b = (const uint16_t*)b;
+    p.y = (uint16_t*)y;
+    p.tiles = qmv_tab;
+    p.M = L.Mmax;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.G = (int)(K / gs);
+    p.part_rows = (int)R;
+    rc = qmv_launch(st, L.qc, p, bits, gs, L.qmv_cap);
+    if (rc) return rc;
+  }
+  if (L.qmm_cap > 0) {
+    QmmParams p{};
+    p.x = (const uint16_t*)x;
+    p.w = w;
+    p.s = (const uint16_t*)s;
+    p.b = (const uint16_t*)b;
+    p.y = (uint16_t*)y;
+    p.tiles = qmm_tab;
+    p.M = (int)R;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.G = (int)(K / gs);
+    rc = qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
+    if (rc) return rc;
+  }
+  return LISAQ_OK;
+}
+
+int lisaq_swiglu(void* stream, const void* gate, const void* up, void* act, int64_t n) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(n >= 0, LISAQ_EINVAL_SHAPE, "swiglu: negative size");
+  if (n == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(gate && up && act, LISAQ_EINVAL_LAYOUT, "swiglu: null tensor pointer");
+  return launch_swiglu((hipStream_t)stream, (const uint16_t*)gate, (const uint16_t*)up, (uint16_t*)act, n);
+}
+
+int lisaq_moe_combine(void* stream, const void* down, const float* wts, const int32_t* inv, void* out, int64_t T,
+                      int k, int64_t H) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(T >= 0 && H >= 0, LISAQ_EINVAL_SHAPE, "moe_combine: negative size");
+  LISAQ_REQUIRE(k >= 1 && k <= 32, LISAQ_EINVAL_SHAPE, "moe_combine: need 1 <= k <= 32 (k=%d)", k);
+  if (T == 0 || H == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(down && wts && inv && out, LISAQ_EINVAL_LAYOUT, "moe_combine: null tensor pointer");
+  return launch_combine((hipStream_t)stream, (const uint16_t*)down, wts, inv, (uint16_t*)out, T, k, H);
+}
+
+// MoE forward workspace: [routing ints][x_sorted][gate_out][up_out][down_sorted][gather ws]
+struct MoeLayout {
+  size_t idx, wts, sorted, order, rows, inv, offs, xs, g, u, d, gws, total;
+};
+
+static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
+  MoeLayout L{};
+  const int64_t R = T * k;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += up256(bytes);
+    return at;
+  };
+  L.idx = take((size_t)R * 4);
+  L.wts = take((size_t)R * 4);
+  L.sorted = take((size_t)R * 4);
+  L.order = take((size_t)R * 4);
+  L.rows = take((size_t)R * 4);
+  L.inv = take((size_t)R * 4);
+  L.offs = take((size_t)(E + 1) * 4);
+  L.xs = take((size_t)R * H * 2);
+  L.g = take((size_t)R * I * 2);
+  L.u = take((size_t)R * I * 2);
+  L.d = take((size_t)R * H * 2);
+  const size_t g1 = lisaq_gather_qmm_workspace(R, I, H, E, gs, bits);
+  const size_t g2 = lisaq_gather_qmm_workspace(R, H, I, E, gs, bits);
+  L.gws = take(g1 > g2 ? g1 : g2);
+  L.total = o;
+  return L;
+}
+
+size_t lisaq_moe_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
+  if (T <= 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 256;
+  return moe_layout(T, H, I, E, k, gs, bits).total;
+}
+
+int lisaq_moe_forward(void* stream, const void* x, const float* logits, const uint32_t* gw, const void* gsc,
+                      const void* gbi, const uint32_t* uw, const void* usc, const void* ubi, const uint32_t* dw,
+                      const void* dsc, const void* dbi, void* out, int64_t T, int64_t H, int64_t I, int E, int k,
+                      int gs, int bits, int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(T >= 0 && H > 0 && I > 0, LISAQ_EINVAL_SHAPE, "moe_forward: bad sizes");
+  if (T == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(x && logits && gw && gsc && gbi && uw && usc && ubi && dw && dsc && dbi && out,
+                LISAQ_EINVAL_LAYOUT, "moe_forward: null tensor pointer");
+  const MoeLayout L = moe_layout(T, H, I, E, k, gs, bits);
+  LISAQ_REQUIRE(ws != nullptr && ws_bytes >= L.total && aligned(ws, 256), LISAQ_EWORKSPACE,
+                "moe_forward: 256-byte aligned workspace of %zu bytes required (got %zu)", L.total, ws_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  char* B = (char*)ws;
+  const int64_t R = T * k;
+  int32_t* idx = topk_idx ? topk_idx : (int32_t*)(B + L.idx);
+  float* wts = topk_w ? topk_w : (float*)(B + L.wts);
+  int32_t* sorted = (int32_t*)(B + L.sorted);
+  int32_t* order = (int32_t*)(B + L.order);
+  int32_t* rows = (int32_t*)(B + L.rows);
+  int32_t* inv = (int32_t*)(B + L.inv);
+  int32_t* offs = (int32_t*)(B + L.offs);
+  uint16_t* xs = (uint16_t*)(B + L.xs);
+  uint16_t* g = (uint16_t*)(B + L.g);
+  uint16_t* u = (uint16_t*)(B + L.u);
+  uint16_t* d = (uint16_t*)(B + L.d);
+  void* gws = B + L.gws;
+  const size_t gws_bytes = L.total - L.gws;
+  int rc;
+  if ((rc = lisaq_moe_route(st, logits, T, E, k, idx, wts))) return rc;
+  if ((rc = lisaq_moe_sort(st, idx, R, E, k, sorted, order, rows, inv, offs))) return rc;
+  if ((rc = lisaq_gather_rows(st, x, rows, xs, R, H))) return rc;
+  if ((rc = lisaq_gather_qmm(st, xs, gw, gsc, gbi, sorted, g, R, I, H, E, 1, gs, bits, gws, gws_bytes))) return rc;
+  if ((rc = lisaq_gather_qmm(st, xs, uw, usc, ubi, sorted, u, R, I, H, E, 1, gs, bits, gws, gws_bytes))) return rc;
+  if ((rc = lisaq_swiglu(st, g, u, g, R * I))) return rc;
+  if ((rc = lisaq_gather_qmm(st, g, dw, dsc, dbi, sorted, d, R, H, I, E, 1, gs, bits, gws, gws_bytes))) return rc;
+  return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
+}
+
+}  // extern "C"

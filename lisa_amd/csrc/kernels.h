@@ -1,0 +1,23 @@
+// Internal launchers of the element-wise / routing kernels (not the C ABI).
+#pragma once
+#include "lisaq_common.h"
+
+namespace lisaq {
+
+int launch_dequantize(hipStream_t st, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                      uint16_t* out, int64_t rows, int64_t K, int gs, int bits);
+int launch_quantize(hipStream_t st, const void* w, int dtype, uint32_t* wq, void* s, void* b,
+                    int64_t rows, int64_t K, int gs, int bits);
+int launch_route(hipStream_t st, const float* logits, int64_t T, int E, int k, int32_t* idx,
+                 float* wts);
+int launch_sort(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,
+                int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets);
+int launch_gather_rows(hipStream_t st, const uint16_t* x, const int32_t* rows, uint16_t* out,
+                       int64_t R, int64_t H);
+int launch_swiglu(hipStream_t st, const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n);
+int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const int32_t* inv,
+                   uint16_t* out, int64_t T, int k, int64_t H);
+int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int N, int limit, int BM, int BN,
+                      int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap, int32_t* counts);
+
+}  // namespace lisaq

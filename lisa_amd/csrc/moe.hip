@@ -1,0 +1,352 @@
+// MoE routing, stable gather permutation, row gather, SwiGLU, sorted combine,
+// and the gather_qmm tile table (gfx950).
+//
+// Reference: crates/lisa-engine/src/models/qwen4/moe.rs:352-449 (generic
+// SparseMoeBlock path), crates/lisa-mlx/src/jit/sort.rs:12-20 (stable argsort),
+// crates/lisa-mlx/src/models/qwen4/kernels/moe.rs:38-242 (combine, counting
+// sort), crates/lisa-mlx/src/shaders/common/exact_header.metal:2-24.
+#include "lisaq_common.h"
+#include "kernels.h"
+
+namespace lisaq {
+
+// ---------------------------------------------------------------------------
+// Router: one wave per token.  Top-k = the first k of a stable ascending sort
+// of -logits: largest logit first, equal logits in increasing expert order.
+// Each of the k rounds takes the wave-wide (max value, min index) among the
+// experts not yet taken.  Softmax over the k selected logits in f32:
+// e = exp(l - max), w = e * (1/sum) (softmax_single_row's normalizer).
+__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int64_t T,
+                                                    int E, int k, int32_t* __restrict__ idx,
+                                                    float* __restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  constexpr int PER = 16;  // E <= 1024
+  const float* l = logits + t * E;
+  float v[PER];
+  uint32_t taken = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? l[e] : -INFINITY;
+    if (e >= E) taken |= 1u << i;
+  }
+  float sel[32];
+  int sid[32];
+  for (int r = 0; r < k; ++r) {
+    float best = 0.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      if (taken & (1u << i)) continue;
+      if (bi == 0x7fffffff || v[i] > best) {  // scanning e upward keeps the lower id on ties
+        best = v[i];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ob = __shfl_xor(best, off);
+      const int oi = __shfl_xor(bi, off);
+      const bool take = (oi != 0x7fffffff) && (bi == 0x7fffffff || ob > best || (!(ob < best) && oi < bi));
+      if (take) {
+        best = ob;
+        bi = oi;
+      }
+    }
+    if ((bi & 63) == lane && bi != 0x7fffffff) taken |= 1u << (bi >> 6);
+    sel[r] = best;
+    sid[r] = bi;
+  }
+  if (lane == 0) {
+    float mx = sel[0];
+    for (int r = 1; r < k; ++r) mx = (mx < sel[r]) ? sel[r] : mx;
+    float ex[32], sum = 0.f;
+    for (int r = 0; r < k; ++r) {
+      ex[r] = expf(sel[r] - mx);
+      sum += ex[r];
+    }
+    const float inv = 1.0f / sum;
+    for (int r = 0; r < k; ++r) {
+      idx[t * k + r] = sid[r];
+      wts[t * k + r] = ex[r] * inv;
+    }
+  }
+}
+
+int launch_route(hipStream_t st, const float* logits, int64_t T, int E, int k, int32_t* idx,
+                 float* wts) {
+  if (T == 0) return LISAQ_OK;
+  hipLaunchKernelGGL(route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, T, E, k, idx,
+                     wts);
+  return check_launch("moe_route");
+}
+
+// ---------------------------------------------------------------------------
+// Stable counting sort of R expert ids in one workgroup of 1024 threads.
+// Pass 1 counts per expert; pass 2 walks the ids in chunks of 1024 and gives
+// each id the position running[e] + (ids of e in earlier waves of the chunk)
+// + (ids of e in earlier lanes of its wave).  Lanes with the same id are
+// found with one ballot per id bit, so the order is the input order (stable)
+// and the result is deterministic.
+__global__ __launch_bounds__(1024) void sort_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
+                                                    int top_k, int32_t* __restrict__ sorted_idx,
+                                                    int32_t* __restrict__ order,
+                                                    int32_t* __restrict__ token_rows,
+                                                    int32_t* __restrict__ inverse,
+                                                    int32_t* __restrict__ offsets) {
+  extern __shared__ int32_t sm[];
+  int32_t* running = sm;          // [E+1]
+  int32_t* wcnt = sm + (E + 1);   // [16][E]
+  __shared__ int bad;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e <= E; e += 1024) running[e] = 0;
+  for (int e = tid; e < 16 * E; e += 1024) wcnt[e] = 0;
+  if (tid == 0) bad = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < R; i += 1024) {
+    const int e = ids[i];
+    if (e < 0 || e >= E) bad = 1;
+    else atomicAdd(&running[e + 1], 1);
+  }
+  __syncthreads();
+  if (bad) {
+    if (tid == 0) offsets[E] = -1;
+    return;
+  }
+  // inclusive scan of running[1..E] -> exclusive offsets in running[0..E]
+  if (tid == 0) {
+    int acc = 0;
+    for (int e = 0; e <= E; ++e) {
+      acc += running[e];
+      running[e] = acc;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += 1024) offsets[e] = running[e];
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  __syncthreads();
+  for (int64_t base = 0; base < R; base += 1024) {
+    const int64_t i = base + tid;
+    const bool valid = i < R;
+    const int e = valid ? ids[i] : -1;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t ones = __ballot(valid && ((e >> b) & 1));
+      peers &= ((e >> b) & 1) ? ones : ~ones;
+    }
+    const uint64_t lower = peers & ((1ull << lane) - 1ull);
+    const int rank = __popcll(lower);
+    const bool leader = valid && lower == 0;  // first lane of its id in this wave
+    if (leader) wcnt[wave * E + e] = __popcll(peers);
+    __syncthreads();
+    int pos = 0;
+    if (valid) {
+      pos = running[e] + rank;
+      for (int w2 = 0; w2 < wave; ++w2) pos += wcnt[w2 * E + e];
+      sorted_idx[pos] = e;
+      order[pos] = (int32_t)i;
+      token_rows[pos] = (int32_t)(i / top_k);
+      inverse[i] = pos;
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&running[e], __popcll(peers));
+      wcnt[wave * E + e] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+int launch_sort(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,
+                int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets) {
+  const size_t lds = sizeof(int32_t) * (size_t)(E + 1 + 16 * E);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return set_error(LISAQ_EHIP, "moe_sort: LDS %zu bytes: %s", lds, hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(1024), lds, st, ids, R, E, top_k, sorted_idx, order,
+                     token_rows, inverse, offsets);
+  return check_launch("moe_sort");
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __restrict__ x,
+                                                          const int32_t* __restrict__ rows,
+                                                          uint16_t* __restrict__ out, int64_t R,
+                                                          int64_t H8) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= R * H8) return;
+  const int64_t r = i / H8, c = i - r * H8;
+  reinterpret_cast<u32x4*>(out)[i] = reinterpret_cast<const u32x4*>(x)[(int64_t)rows[r] * H8 + c];
+}
+
+__global__ __launch_bounds__(256) void gather_rows_scalar_kernel(const uint16_t* __restrict__ x,
+                                                                 const int32_t* __restrict__ rows,
+                                                                 uint16_t* __restrict__ out, int64_t R,
+                                                                 int64_t H) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= R * H) return;
+  const int64_t r = i / H, c = i - r * H;
+  out[i] = x[(int64_t)rows[r] * H + c];
+}
+
+int launch_gather_rows(hipStream_t st, const uint16_t* x, const int32_t* rows, uint16_t* out, int64_t R,
+                       int64_t H) {
+  if (R == 0 || H == 0) return LISAQ_OK;
+  if (H % 8 == 0) {
+    const int64_t n = R * (H / 8);
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, rows, out,
+                       R, H / 8);
+  } else {
+    const int64_t n = R * H;
+    hipLaunchKernelGGL(gather_rows_scalar_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x,
+                       rows, out, R, H);
+  }
+  return check_launch("gather_rows");
+}
+
+// ---------------------------------------------------------------------------
+// act = bf16( bf16(g * bf16(sigmoid(g))) * u ); sigmoid as the MLX unary op:
+// y = 1/(1+exp(|x|)), x<0 ? y : 1-y.
+__device__ __forceinline__ float silu_bf16(float g) {
+  const float y = 1.0f / (1.0f + expf(fabsf(g)));
+  const float sg = bf2f(f2bf(g < 0.0f ? y : 1.0f - y));
+  return bf2f(f2bf(__fmul_rn(g, sg)));
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ g,
+                                                     const uint16_t* __restrict__ u,
+                                                     uint16_t* __restrict__ out, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = f2bf(__fmul_rn(silu_bf16(bf2f(g[i])), bf2f(u[i])));
+}
+
+int launch_swiglu(hipStream_t st, const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n) {
+  if (n == 0) return LISAQ_OK;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n);
+  return check_launch("swiglu");
+}
+
+// ---------------------------------------------------------------------------
+// Sorted combine with the colsum_small<K> association (exact_header.metal:12-24):
+// TY = min(K,8); t[y] = sum_{rr = y; rr < K; rr += TY} (prod[rr] + acc);
+// total = t[0]; total = t[j] + total.  Multiplies and adds are separately
+// rounded (no contraction) so the result is bit-identical to the reference.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ down,
+                                                      const float* __restrict__ w,
+                                                      const int32_t* __restrict__ inv,
+                                                      uint16_t* __restrict__ out, int64_t T, int k,
+                                                      int64_t H) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= T * H) return;
+  const int64_t t = i / H, d = i - t * H;
+  const int TY = k < 8 ? k : 8;
+  float tt[8];
+  for (int y = 0; y < TY; ++y) {
+    float acc = 0.0f;
+    for (int rr = y; rr < k; rr += TY) {
+      const float prod = __fmul_rn(bf2f(down[(int64_t)inv[t * k + rr] * H + d]), w[t * k + rr]);
+      acc = __fadd_rn(prod, acc);
+    }
+    tt[y] = acc;
+  }
+  float total = tt[0];
+  for (int j = 1; j < TY; ++j) total = __fadd_rn(tt[j], total);
+  out[i] = f2bf(total);
+}
+
+int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const int32_t* inv, uint16_t* out,
+                   int64_t T, int k, int64_t H) {
+  const int64_t n = T * H;
+  if (n == 0) return LISAQ_OK;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, down, w, inv, out,
+                     T, k, H);
+  return check_launch("moe_combine");
+}
+
+// ---------------------------------------------------------------------------
+// gather_qmm tile tables.  Runs of equal consecutive expert ids are found and
+// each run becomes either matvec tiles (run length < limit: {e, start, len,
+// n tile of 32}) or matmul tiles ({e, start + i*BM, rows, n tile of BN}),
+// matching the reference's per-run quantized_matmul dispatch.  Unused entries
+// up to each table's capacity are written as {-1,..} so a grid of `capacity`
+// workgroups can be launched without a host round trip.  One workgroup.
+__global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restrict__ ids, int64_t R,
+                                                          int N, int limit, int BM, int BN,
+                                                          int4* __restrict__ qmv_tab, int qmv_cap,
+                                                          int4* __restrict__ qmm_tab, int qmm_cap,
+                                                          int32_t* __restrict__ counts) {
+  __shared__ int s_qmv[1024], s_qmm[1024], s_tot[2];
+  const int tid = threadIdx.x;
+  const int nt32 = (N + 31) / 32;
+  const int ntbn = (N + BN - 1) / BN;
+  // contiguous segment of the ids per thread
+  const int64_t seg = (R + 1023) / 1024;
+  const int64_t i0 = tid * seg, i1 = (i0 + seg < R) ? i0 + seg : R;
+  // entries produced by runs that START in this segment
+  int cq = 0, cm = 0;
+  for (int64_t i = i0; i < i1; ++i) {
+    if (i > 0 && ids[i] == ids[i - 1]) continue;
+    int64_t j = i + 1;
+    while (j < R && ids[j] == ids[i]) ++j;
+    const int64_t len = j - i;
+    if (len < limit) cq += nt32;
+    else cm += (int)((len + BM - 1) / BM) * ntbn;
+  }
+  s_qmv[tid] = cq;
+  s_qmm[tid] = cm;
+  __syncthreads();
+  if (tid == 0) {
+    int a = 0, b = 0;
+    for (int t = 0; t < 1024; ++t) {
+      const int x = s_qmv[t], y = s_qmm[t];
+      s_qmv[t] = a;
+      s_qmm[t] = b;
+      a += x;
+      b += y;
+    }
+    counts[0] = a;
+    counts[1] = b;
+    s_tot[0] = a;
+    s_tot[1] = b;
+    counts[2] = (a > qmv_cap || b > qmm_cap) ? 1 : 0;  // overflow: ids not sorted
+  }
+  __syncthreads();
+  int oq = s_qmv[tid], om = s_qmm[tid];
+  for (int64_t i = i0; i < i1; ++i) {
+    if (i > 0 && ids[i] == ids[i - 1]) continue;
+    int64_t j = i + 1;
+    while (j < R && ids[j] == ids[i]) ++j;
+    const int64_t len = j - i;
+    const int e = ids[i];
+    if (len < limit) {
+      for (int nt = 0; nt < nt32; ++nt, ++oq)
+        if (oq < qmv_cap) qmv_tab[oq] = make_int4(e, (int)i, (int)len, nt);
+    } else {
+      for (int64_t r0 = 0; r0 < len; r0 += BM)
+        for (int nt = 0; nt < ntbn; ++nt, ++om) {
+          const int rows = (int)((len - r0) < BM ? (len - r0) : BM);
+          if (om < qmm_cap) qmm_tab[om] = make_int4(e, (int)(i + r0), rows, nt);
+        }
+    }
+  }
+  __syncthreads();
+  const int a = s_tot[0], b = s_tot[1];
+  for (int t = a + tid; t < qmv_cap; t += 1024) qmv_tab[t] = make_int4(-1, 0, 0, 0);
+  for (int t = b + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
+}
+
+int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int N, int limit, int BM, int BN,
+                      int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap, int32_t* counts) {
+  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), 0, st, ids, R, N, limit, BM, BN, qmv_tab,
+                     qmv_cap, qmm_tab, qmm_cap, counts);
+  return check_launch("gather_tile_table");
+}
+
+}  // namespace lisaq

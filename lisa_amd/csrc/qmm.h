@@ -1,0 +1,25 @@
+// Internal interface of the qmm kernels (not part of the C ABI).
+#pragma once
+#include "lisaq_common.h"
+
+namespace lisaq {
+
+struct QmmParams {
+  const uint16_t* x;   // [rows, K] bf16
+  const uint32_t* w;   // [(E,) N, K/pack]
+  const uint16_t* s;   // [(E,) N, G] bf16
+  const uint16_t* b;   // [(E,) N, G] bf16
+  uint16_t* y;         // [rows, N] bf16
+  const int4* tiles;   // gather: {expert, row start, rows, n tile} per block, or null
+  int M, N, K, G;
+};
+
+struct QmmConfig {
+  int MT, NT, BM, BN, grid_n, grid_m;
+};
+
+QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
+               int grid_y);
+
+}  // namespace lisaq

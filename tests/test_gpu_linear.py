@@ -1,0 +1,190 @@
+"""GPU parity of quantized_matmul (matvec and matmul paths), dequantize and
+quantize against the CPU oracle, through the C ABI (lisa_amd.ops -> liblisaq).
+
+Tolerance for outputs: |got - ref| <= 2e-2 + 1e-2*|ref| per element (the
+north-star bound; see tests/_util.py).  Integer work (codes, quantize output,
+dequantize bits) is compared bit-exactly."""
+import numpy as np
+import pytest
+
+from lisa_amd import ops
+from lisa_amd.synth import bf16_bits_to_f32, np_linear, np_x
+from tests._util import assert_close_bf16, from_dev_bf16, to_dev, to_dev_bf16, to_dev_u32
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(fn, dev, x, w, s, b, gs, bits):
+    y = fn(to_dev_bf16(x, dev), to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev),
+           group_size=gs, bits=bits)
+    return from_dev_bf16(y)
+
+
+QMV_CASES = [
+    # (M, N, K, bits, gs)
+    (1, 3072, 1024, 4, 64),      # configs[0]
+    (1, 256, 512, 4, 64),
+    (3, 64, 512, 4, 64),         # array_ops.rs:650-710 shape
+    (1, 100, 512, 4, 64),        # N tail (not a multiple of 32)
+    (5, 77, 320, 4, 64),         # K/gs = 5 groups (U = 1 path), N tail
+    (2, 9728, 2560, 4, 64),      # configs[1] up
+    (8, 2560, 9728, 4, 64),      # configs[1] down (split over K)
+    (4, 2560, 9728, 4, 64),
+    (1, 512, 1024, 2, 64),
+    (8, 640, 2048, 2, 64),
+    (1, 256, 1024, 4, 32),
+    (3, 256, 1024, 4, 128),
+    (1, 256, 1024, 2, 32),
+    (2, 256, 1024, 2, 128),
+    (12, 1024, 1024, 4, 64),     # MQ = 2
+    (20, 512, 2048, 4, 64),      # MQ = 3
+    (32, 512, 1024, 4, 64),      # MQ = 4 (forced qmv)
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs", QMV_CASES)
+def test_qmv_parity(dev, oracle, M, N, K, bits, gs):
+    rng = np.random.default_rng(M * 7 + N + K + bits + gs)
+    w, s, b = np_linear(rng, N, K, bits, gs, s_std=0.02 if bits == 4 else 0.05,
+                        b_std=0.01 if bits == 4 else 0.02)
+    x = np_x(rng, M, K)
+    ref = oracle.qmv(x, w, s, b, gs, bits)
+    got = _run(ops.qmv, dev, x, w, s, b, gs, bits)
+    assert_close_bf16(got, ref, what=f"qmv M={M} N={N} K={K} bits={bits} gs={gs}")
+    if M < ops.qmv_batch_limit(K, N):
+        got2 = _run(ops.quantized_matmul, dev, x, w, s, b, gs, bits)
+        assert np.array_equal(got, got2)
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs", [
+    (33, 256, 512, 4, 64), (64, 256, 1024, 4, 64), (130, 300, 512, 4, 64), (128, 512, 2048, 2, 64),
+    (96, 256, 1024, 4, 32), (50, 256, 1024, 4, 128), (200, 1024, 768, 4, 64), (13, 256, 4096, 2, 128),
+])
+def test_qmm_parity(dev, oracle, M, N, K, bits, gs):
+    rng = np.random.default_rng(M + N + K + bits * 3 + gs)
+    w, s, b = np_linear(rng, N, K, bits, gs)
+    x = np_x(rng, M, K)
+    ref = oracle.qmm(x, w, s, b, gs, bits)
+    got = _run(ops.qmm, dev, x, w, s, b, gs, bits)
+    assert_close_bf16(got, ref, what=f"qmm M={M} N={N} K={K} bits={bits} gs={gs}")
+    if M >= ops.qmv_batch_limit(K, N):
+        got2 = _run(ops.quantized_matmul, dev, x, w, s, b, gs, bits)
+        assert np.array_equal(got, got2)
+
+
+@pytest.mark.parametrize("M,N,K,bits", [(128, 17408, 5120, 4), (512, 5120, 17408, 4), (2048, 17408, 5120, 4),
+                                        (512, 17408, 5120, 2)])
+def test_qmm_prefill_shapes_sampled_rows(dev, oracle, M, N, K, bits):
+    """configs[2]/[3] prefill shapes; the oracle checks 8 sampled rows (every column)."""
+    import torch
+
+    rng = np.random.default_rng(M + N)
+    w, s, b = np_linear(rng, N, K, bits, 64, s_std=0.02 if bits == 4 else 0.05, b_std=0.01 if bits == 4 else 0.02)
+    x = np_x(rng, M, K)
+    y = ops.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev),
+                             group_size=64, bits=bits)
+    torch.cuda.synchronize()
+    rows = np.sort(rng.choice(M, 8, replace=False))
+    rows[0], rows[-1] = 0, M - 1
+    ref = oracle.qmm(x[rows], w, s, b, 64, bits)
+    got = from_dev_bf16(y)[rows]
+    assert_close_bf16(got, ref, what=f"prefill M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_north_star_qmv_shape(dev, oracle, bits):
+    rng = np.random.default_rng(17408 + bits)
+    N, K = 17408, 5120
+    w, s, b = np_linear(rng, N, K, bits, 64, s_std=0.02 if bits == 4 else 0.05, b_std=0.01 if bits == 4 else 0.02)
+    for M in (1, 8):
+        x = np_x(rng, M, K)
+        ref = oracle.qmv(x, w, s, b, 64, bits)
+        got = _run(ops.quantized_matmul, dev, x, w, s, b, 64, bits)
+        assert_close_bf16(got, ref, what=f"north-star qmv M={M} bits={bits}")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_serial_rows_bitwise_equal_to_single_rows(dev, bits):
+    """array_ops.rs:650-710: batched rows == independent M=1 calls, bitwise."""
+    rng = np.random.default_rng(99 + bits)
+    for N, K in ((64, 512), (2560, 9728), (9728, 2560)):
+        w, s, b = np_linear(rng, N, K, bits, 64)
+        x = np_x(rng, 3, K)
+        batched = _run(ops.quantized_matmul_serial_rows, dev, x, w, s, b, 64, bits)
+        for r in range(3):
+            one = _run(ops.quantized_matmul, dev, x[r:r + 1], w, s, b, 64, bits)
+            assert np.array_equal(batched[r:r + 1], one), (N, K, r)
+
+
+def test_repeated_calls_deterministic(dev):
+    """Split-K partials are summed in slab order: identical bits every call."""
+    rng = np.random.default_rng(5)
+    w, s, b = np_linear(rng, 2560, 9728)
+    x = np_x(rng, 4, 9728)
+    first = _run(ops.quantized_matmul, dev, x, w, s, b, 64, 4)
+    for _ in range(3):
+        assert np.array_equal(_run(ops.quantized_matmul, dev, x, w, s, b, 64, 4), first)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (2, 64), (4, 32), (2, 128), (8, 64)])
+def test_dequantize_bit_exact(dev, oracle, bits, gs):
+    rng = np.random.default_rng(bits * gs)
+    N, K = 300, 1024
+    w, s, b = np_linear(rng, N, K, bits, gs)
+    got = from_dev_bf16(ops.dequantize(to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev), gs, bits))
+    ref = oracle.f32_to_bf16(oracle.dequantize(w, s, b, gs, bits))
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_quantize_bit_exact_f32(dev, oracle, bits):
+    import torch
+
+    from lisa_amd.synth import lcg_array
+
+    N, K, gs = 64, 512, 64
+    wf = lcg_array(0x2F1D4A73, N * K).reshape(N, K)
+    wf[0, :64] = 0.0  # all-zero group
+    wf[1, :64] = -np.abs(wf[1, :64]) - 0.1  # all-negative group
+    wq, sc, bi = ops.quantize(to_dev(wf, dev), gs, bits)
+    rq, rs, rb = oracle.quantize_f32(wf, gs, bits)
+    assert np.array_equal(wq.cpu().numpy().view(np.uint32), rq)
+    assert np.array_equal(sc.cpu().numpy(), rs) and np.array_equal(bi.cpu().numpy(), rb)
+    # bf16 input: scales/biases rounded to bf16 like to_dtype(wdt)
+    wb = torch.from_numpy(wf).to(torch.bfloat16)
+    wbf = wb.float().numpy()
+    wq2, sc2, bi2 = ops.quantize(wb.to(dev), gs, bits)
+    rq2, rs2, rb2 = oracle.quantize_f32(wbf, gs, bits)
+    assert np.array_equal(wq2.cpu().numpy().view(np.uint32), rq2)
+    assert np.array_equal(from_dev_bf16(sc2), oracle.f32_to_bf16(rs2))
+    assert np.array_equal(from_dev_bf16(bi2), oracle.f32_to_bf16(rb2))
+
+
+def test_quantize_then_matmul_smoke(dev):
+    """smoke.rs:19-40 with our ops: quantize -> quantized_matmul vs dequantize -> matmul (max |d| < 0.1)."""
+    import torch
+
+    from lisa_amd.synth import lcg_array
+
+    w = torch.from_numpy(lcg_array(42, 64 * 256).reshape(64, 256)).to(dev)
+    x = torch.from_numpy(lcg_array(7, 256).reshape(1, 256)).to(dev).to(torch.bfloat16)
+    wq, sc, bi = ops.quantize(w, 32, 4)
+    y1 = ops.quantized_matmul(x, wq, sc.to(torch.bfloat16), bi.to(torch.bfloat16), True, 32, 4)
+    wd = ops.dequantize(wq, sc.to(torch.bfloat16), bi.to(torch.bfloat16), 32, 4)
+    y2 = (x.float() @ wd.float().T)
+    assert (y1.float() - y2).abs().max().item() < 0.1
+
+
+def test_rejections_raise(dev):
+    rng = np.random.default_rng(0)
+    w, s, b = np_linear(rng, 64, 128)
+    x = np_x(rng, 1, 128)
+    with pytest.raises(ops.LisaqError, match="biases"):
+        ops.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(w, dev), to_dev_bf16(s, dev), None)
+    with pytest.raises(ops.LisaqError, match="transpose"):
+        ops.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev),
+                             transpose=False)
+    import torch
+    with pytest.raises(ops.LisaqError, match="dtype"):
+        ops.quantized_matmul(torch.zeros(1, 128, device=dev), to_dev_u32(w, dev), to_dev_bf16(s, dev),
+                             to_dev_bf16(b, dev))
