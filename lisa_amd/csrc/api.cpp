@@ -118,7 +118,7 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   if (L.Mmax < 1) L.Mmax = 1;
   L.qc = qmv_config(L.Mmax, N, K, gs, bits, /*single_pass=*/true);
   L.mc = qmm_config(L.limit, N, K, gs, bits);
-  L.qmv_cap = (int)(runs * ((N + 31) / 32));
+  L.qmv_cap = (int)(runs * ((N + L.qc.tile_rows - 1) / L.qc.tile_rows));
   L.qmm_cap = (R >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
   L.qmv_off = 256;
   L.qmm_off = L.qmv_off + up256((size_t)L.qmv_cap * 16);
@@ -228,7 +228,8 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
   // row the arithmetic of an independent M=1 call.
   const QmvConfig c = qmv_config(1, N, K, gs, bits);
   QmvConfig cm = c;
-  cm.lds_bytes = qmv_lds_bytes(c.slab_groups, gs, (int)M, 1, bits, c.NW);
+  cm.MR = M == 1 ? 1 : (M == 2 ? 2 : 4);  // accumulator rows in use; per-row arithmetic unchanged
+  cm.lds_bytes = qmv_lds_bytes_for(c, gs, (int)M, bits);
   cm.ws_bytes = c.S > 1 ? kQmvCounterBytes + (size_t)c.S * M * N * 4 : 0;
   if (cm.lds_bytes <= 64 * 1024)
     return run_qmv((hipStream_t)stream, cm, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
@@ -326,8 +327,8 @@ int lisaq_gather_qmm(void* stream, const void* x, const uint32_t* w, const void*
   int32_t* counts = (int32_t*)base;
   int4* qmv_tab = (int4*)(base + L.qmv_off);
   int4* qmm_tab = (int4*)(base + L.qmm_off);
-  rc = launch_tile_table(st, rhs, R, (int)N, L.limit, L.mc.BM, L.mc.BN, qmv_tab, L.qmv_cap, qmm_tab, L.qmm_cap,
-                         counts);
+  rc = launch_tile_table(st, rhs, R, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN, qmv_tab, L.qmv_cap, qmm_tab,
+                         L.qmm_cap, counts);
   if (rc) return rc;
   if (L.qmv_cap > 0) {
     QmvParams p{};

@@ -278,13 +278,13 @@ int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const i
 // up to each table's capacity are written as {-1,..} so a grid of `capacity`
 // workgroups can be launched without a host round trip.  One workgroup.
 __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restrict__ ids, int64_t R,
-                                                          int N, int limit, int BM, int BN,
+                                                          int N, int limit, int VR, int BM, int BN,
                                                           int4* __restrict__ qmv_tab, int qmv_cap,
                                                           int4* __restrict__ qmm_tab, int qmm_cap,
                                                           int32_t* __restrict__ counts) {
   __shared__ int s_qmv[1024], s_qmm[1024], s_tot[2];
   const int tid = threadIdx.x;
-  const int nt32 = (N + 31) / 32;
+  const int nt32 = (N + VR - 1) / VR;  // matvec tiles of VR rows
   const int ntbn = (N + BN - 1) / BN;
   // contiguous segment of the ids per thread
   const int64_t seg = (R + 1023) / 1024;
@@ -342,9 +342,9 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   for (int t = b + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
 }
 
-int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int N, int limit, int BM, int BN,
+int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int N, int limit, int VR, int BM, int BN,
                       int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap, int32_t* counts) {
-  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), 0, st, ids, R, N, limit, BM, BN, qmv_tab,
+  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), 0, st, ids, R, N, limit, VR, BM, BN, qmv_tab,
                      qmv_cap, qmm_tab, qmm_cap, counts);
   return check_launch("gather_tile_table");
 }

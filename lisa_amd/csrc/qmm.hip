@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t xt[2][BM * XS];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int col = lane & 31;
   const int h = lane >> 5;
 

@@ -18,6 +18,7 @@ struct QmvParams {
   int part_rows;         // rows of the partial buffer
   int S, S_inner;        // slabs across workgroups (grid y) / walked inside one
   int slab_groups;       // groups per slab
+  int debug;             // experiment builds only: phases to skip
   // filled by qmv_launch from the config
 };
 
@@ -28,7 +29,10 @@ constexpr int kQmvMaxTiles = 32768;
 constexpr size_t kQmvCounterBytes = (size_t)kQmvMaxTiles * 4;
 
 struct QmvConfig {
+  int kind;       // 0: 32-row tiles (mfma 32x32x16), 1: 16-row tiles, 2: streaming 16-row tiles
+  int tile_rows;  // rows of W per workgroup (32 or 16)
   int U, MQ, NW, S, S_inner, slab_groups, tiles, lds_bytes;
+  int MR;         // streaming kernel: accumulator rows per lane group in use (1, 2 or 4)
   size_t ws_bytes;       // kQmvCounterBytes + partials (0 when S == 1)
 };
 
@@ -37,8 +41,21 @@ struct QmvConfig {
 // no workspace): the gather path uses it.
 QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass = false);
 
-// Dynamic LDS bytes of a launch with the given slab size.
-int qmv_lds_bytes(int slab_groups, int gs, int M, int MQ, int bits, int NW);
+// Dynamic LDS bytes of launch `c` when run with M rows (same slabs and waves).
+int qmv_lds_bytes_for(const QmvConfig& c, int gs, int M, int bits);
+
+// Kernel-specific halves (qmv.hip: 32-row tiles, qmv16.hip: 16-row tiles).
+QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass);
+int qmv32_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
+int qmv32_lds_bytes(int slab_groups, int gs, int M, int MQ, int bits, int NW);
+bool qmv16_supported(int64_t M, int gs, int bits);
+QmvConfig qmv16_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+int qmv16_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
+int qmv16_lds_bytes(int SG, int gs, int M, int MQ, int bits, int NW);
+bool qmvt_supported(int64_t M, int64_t K, int gs, int bits);
+QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
+int qmvt_lds_bytes(const QmvConfig& c, int gs, int M, int bits);
 
 // Enqueue; grid_x = number of row tiles (or tile-table entries).
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);

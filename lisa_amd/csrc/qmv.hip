@@ -166,7 +166,7 @@ __global__ __launch_bounds__(512) void qmv_kernel(QmvParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int NW = blockDim.x >> 6;
   const int col = lane & 31;  // output row n within the tile / x row m
   const int h = lane >> 5;    // half of the group along K
@@ -243,66 +243,64 @@ __global__ __launch_bounds__(512) void qmv_kernel(QmvParams p) {
   };
   if (c < nchunks) load_chunk(c, wcur, scur, bcur);
 
-  // --- stage x (permuted to the unpack order, pre-scaled) into LDS
+  // --- stage x (permuted to the unpack order, pre-scaled) into LDS.
+  // One thread per (row m, group, half); the two halves of a group sit in
+  // adjacent lanes so the group sums combine with one lane exchange.
   {
-    const int per_row = GL * G::NJ * 2;
-    const int entries = per_row * M;
-    for (int idx = threadIdx.x; idx < entries; idx += blockDim.x) {
-      const int m = idx / per_row;
-      int r = idx - m * per_row;
-      const int hh = r & 1;
-      r >>= 1;
-      const int j = r % G::NJ;
-      const int gl = r / G::NJ;
-      const uint16_t* xr = x + (int64_t)m * p.K + (int64_t)(g_begin + gl) * GS + hh * (GS / 2);
-      uint32_t v[4];
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        int k0, k1;
-        float f0, f1;
-        slot_of<BITS>(j, 2 * e2, k0, f0);
-        slot_of<BITS>(j, 2 * e2 + 1, k1, f1);
-        uint16_t a = xr[k0], b = xr[k1];
-        if (BITS == 2) {
-          a = f2bf(bf2f(a) * f0);
-          b = f2bf(bf2f(b) * f1);
-        }
-        v[e2] = (uint32_t)a | ((uint32_t)b << 16);
-      }
-      xl[m * RS + (gl * G::NJ + j) * 2 + hh] = u32x4{v[0], v[1], v[2], v[3]};
-    }
-  }
-  __syncthreads();
-  // per (group, quad, half): float4 of sum(x) [and sum(x~) for 2-bit] over
-  // rows m = 8q + 4h + i (zero for m >= M)
-  {
-    const int entries = GL * MQ * 2 * 4;
+    constexpr int HV = GS / 2;      // x values per half group
+    constexpr int HQ = HV / 8;      // uint4 loads per half group
     float* xs = reinterpret_cast<float*>(xs4);
+    const int entries = M * GL * 2;
     for (int idx = threadIdx.x; idx < entries; idx += blockDim.x) {
-      const int i = idx & 3;
-      const int hh = (idx >> 2) & 1;
-      const int q = (idx >> 3) % MQ;
-      const int gl = (idx >> 3) / MQ;
-      const int m = 8 * q + 4 * hh + i;
-      float sx = 0.f, st = 0.f;
-      if (m < M) {
-        for (int j = 0; j < G::NJ; ++j)
-          for (int half = 0; half < 2; ++half) {
-            const u32x4 v = xl[m * RS + (gl * G::NJ + j) * 2 + half];
+      const int hh = idx & 1;
+      const int gl = (idx >> 1) % GL;
+      const int m = (idx >> 1) / GL;
+      const u32x4* src = reinterpret_cast<const u32x4*>(
+          x + (int64_t)m * p.K + (int64_t)(g_begin + gl) * GS + hh * HV);
+      uint32_t raw[HV / 2];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const uint32_t word = v[e >> 1];
-              const float xv = (e & 1) ? bf2f_hi(word) : bf2f_lo(word);
-              int ko;
-              float f;
-              slot_of<BITS>(j, e, ko, f);
-              st += xv;
-              sx += xv / f;
-            }
-          }
+      for (int i = 0; i < HQ; ++i) {
+        const u32x4 v = src[i];
+        raw[4 * i + 0] = v[0];
+        raw[4 * i + 1] = v[1];
+        raw[4 * i + 2] = v[2];
+        raw[4 * i + 3] = v[3];
       }
-      xs[idx] = sx;
-      if (BITS == 2) xs[XT * 4 + idx] = st;
+      float sx = 0.f, st = 0.f;
+#pragma unroll
+      for (int j = 0; j < G::NJ; ++j) {
+        uint32_t o[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          uint32_t pair = 0;
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            int ko;
+            float f;
+            slot_of<BITS>(j, 2 * e2 + half, ko, f);
+            const uint32_t wv = raw[ko >> 1];
+            uint32_t bits16 = (ko & 1) ? (wv >> 16) : (wv & 0xffffu);
+            const float xv = __uint_as_float(bits16 << 16);
+            sx += xv;
+            if (BITS == 2) {
+              const float xt = xv * f;  // f is a power of two: exact
+              bits16 = f2bf(xt);
+              st += xt;
+            }
+            pair |= bits16 << (16 * half);
+          }
+          o[e2] = pair;
+        }
+        xl[m * RS + (gl * G::NJ + j) * 2 + hh] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+      sx += __shfl_xor(sx, 1);
+      if (BITS == 2) st += __shfl_xor(st, 1);
+      if (hh == 0) {
+        const int q = m >> 3, h2 = (m >> 2) & 1, i = m & 3;
+        const int at = ((gl * MQ + q) * 2 + h2) * 4 + i;
+        xs[at] = sx;
+        if (BITS == 2) xs[XT * 4 + at] = st;
+      }
     }
   }
   __syncthreads();
@@ -438,7 +436,7 @@ __global__ __launch_bounds__(512) void qmv_kernel(QmvParams p) {
 
 static int pick_u(int G) { return (G % 4 == 0) ? 4 : 1; }
 
-QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
+QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
   QmvConfig c{};
   const int G = (int)(K / gs);
   const int MQ = (int)((M + 7) / 8);
@@ -497,10 +495,36 @@ QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool sin
     c.S_inner = S_inner;
   }
   c.ws_bytes = (c.S > 1) ? kQmvCounterBytes + (size_t)c.S * M * N * 4 : 0;
+  c.kind = 0;
+  c.tile_rows = 32;
   return c;
 }
 
-int qmv_lds_bytes(int slab_groups, int gs, int M, int MQ, int bits, int NW) {
+// Dispatcher.  The cross-workgroup split over K (S > 1) is kept for
+// completeness but not chosen: publishing partials across workgroups needs
+// agent-scope release/acquire, which on a multi-XCD MI355X writes back and
+// invalidates L2 and measured 3x slower than one pass per row tile.
+QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
+  (void)single_pass;
+  const char* force = getenv("LISAQ_QMV_KERNEL");  // tuning: "32", "16" or "t"
+  const char f = force ? force[0] : 0;
+  if (f != '3' && f != '1' && qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits);
+  if (f != '3' && qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
+  return qmv32_config(M, N, K, gs, bits, true);
+}
+
+int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
+  if (c.kind == 2) return qmvt_launch(stream, c, p, bits, gs, grid_x);
+  return c.kind == 1 ? qmv16_launch(stream, c, p, bits, gs, grid_x) : qmv32_launch(stream, c, p, bits, gs, grid_x);
+}
+
+int qmv_lds_bytes_for(const QmvConfig& c, int gs, int M, int bits) {
+  if (c.kind == 2) return qmvt_lds_bytes(c, gs, M, bits);
+  return c.kind == 1 ? qmv16_lds_bytes(c.slab_groups, gs, M, c.MQ, bits, c.NW)
+                     : qmv32_lds_bytes(c.slab_groups, gs, M, c.MQ, bits, c.NW);
+}
+
+int qmv32_lds_bytes(int slab_groups, int gs, int M, int MQ, int bits, int NW) {
   return qmv_lds_layout(slab_groups, gs, M, MQ, bits, NW).total;
 }
 
@@ -532,8 +556,8 @@ static qmv_fn qmv_kernel_for(int bits, int gs, int MQ, int U) {
   return nullptr;
 }
 
-int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs,
-               int grid_x) {
+int qmv32_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs,
+                 int grid_x) {
   qmv_fn fn = qmv_kernel_for(bits, gs, c.MQ, c.U);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmv: bits=%d group_size=%d not supported", bits, gs);
   p.S = c.S;
