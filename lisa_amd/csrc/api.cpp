@@ -227,6 +227,26 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
   // The M=1 schedule (same slabs, same waves) applied to every row gives each
   // row the arithmetic of an independent M=1 call.
   const QmvConfig c = qmv_config(1, N, K, gs, bits);
+  if (c.kind == 4) {
+    // the one-row kernel: one launch per row
+    for (int64_t r = 0; r < M; ++r) {
+      rc = run_qmv((hipStream_t)stream, c, (const uint16_t*)x + r * K, w, s, b, (uint16_t*)y + r * N, 1, N, K, gs,
+                   bits, ws, ws_bytes);
+      if (rc) return rc;
+    }
+    return LISAQ_OK;
+  }
+  if (c.kind == 3) {
+    // the dot kernel computes every row of a launch with the same arithmetic
+    // (any MR), so pairs of rows share one pass over W
+    for (int64_t r = 0; r < M; r += 2) {
+      const int64_t mr = M - r < 2 ? M - r : 2;
+      rc = run_qmv((hipStream_t)stream, qmvd_config(mr, N, K, gs, bits), (const uint16_t*)x + r * K, w, s, b,
+                   (uint16_t*)y + r * N, mr, N, K, gs, bits, ws, ws_bytes);
+      if (rc) return rc;
+    }
+    return LISAQ_OK;
+  }
   QmvConfig cm = c;
   cm.MR = M == 1 ? 1 : (M == 2 ? 2 : 4);  // accumulator rows in use; per-row arithmetic unchanged
   cm.lds_bytes = qmv_lds_bytes_for(c, gs, (int)M, bits);

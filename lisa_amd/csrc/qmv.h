@@ -19,6 +19,8 @@ struct QmvParams {
   int S, S_inner;        // slabs across workgroups (grid y) / walked inside one
   int slab_groups;       // groups per slab
   int debug;             // experiment builds only: phases to skip
+  int chunks, rpr, tile_rows;  // dot kernel: 32-code chunks per row, rows side by side, rows per tile
+  int sbi;               // dot kernel: 4-element scale/bias staging loads per thread
   // filled by qmv_launch from the config
 };
 
@@ -29,10 +31,14 @@ constexpr int kQmvMaxTiles = 32768;
 constexpr size_t kQmvCounterBytes = (size_t)kQmvMaxTiles * 4;
 
 struct QmvConfig {
-  int kind;       // 0: 32-row tiles (mfma 32x32x16), 1: 16-row tiles, 2: streaming 16-row tiles
+  int kind;       // 0: 32-row tiles (mfma 32x32x16), 1: 16-row tiles, 2: streaming 16-row tiles,
+                  // 3: VALU dot kernel (U = rows per thread, S = rows side by side, S_inner = chunks),
+                  // 4: persistent one-row dot kernel (U = passes, S = ring depth, S_inner = chunks)
   int tile_rows;  // rows of W per workgroup (32 or 16)
   int U, MQ, NW, S, S_inner, slab_groups, tiles, lds_bytes;
   int MR;         // streaming kernel: accumulator rows per lane group in use (1, 2 or 4)
+  int sbi;        // dot kernel: scale/bias staging loads per thread
+  int sbw;        // one-row kernel: bytes per lane of the scale/bias row loads
   size_t ws_bytes;       // kQmvCounterBytes + partials (0 when S == 1)
 };
 
@@ -56,6 +62,12 @@ bool qmvt_supported(int64_t M, int64_t K, int gs, int bits);
 QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
 int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmvt_lds_bytes(const QmvConfig& c, int gs, int M, int bits);
+bool qmvd_supported(int64_t M, int64_t N, int64_t K, int gs, int bits);
+QmvConfig qmvd_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+int qmvd_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
+int qmvd_lds_bytes(const QmvConfig& c, int M);
+QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+int qmvp_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 
 // Enqueue; grid_x = number of row tiles (or tile-table entries).
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);

@@ -505,20 +505,32 @@ QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool s
 // agent-scope release/acquire, which on a multi-XCD MI355X writes back and
 // invalidates L2 and measured 3x slower than one pass per row tile.
 QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
-  (void)single_pass;
-  const char* force = getenv("LISAQ_QMV_KERNEL");  // tuning: "32", "16" or "t"
+  const char* force = getenv("LISAQ_QMV_KERNEL");  // tuning: "32", "16", "t" (streaming), "d" (dot), "p" (persistent)
   const char f = force ? force[0] : 0;
+  // One row: the persistent kernel when there are enough rows to keep every
+  // wave busy (measured), else the workgroup dot kernel; more rows: the MFMA
+  // streaming kernel.
+  if (!single_pass && f != '3' && f != '1' && f != 't' && f != 'd' && M == 1 && (N >= 16384 || f == 'p')) {
+    const QmvConfig c = qmvp_config(M, N, K, gs, bits);
+    if (c.kind == 4) return c;
+  }
+  if (f != '3' && f != '1' && f != 't' && (M == 1 || f == 'd') && qmvd_supported(M, N, K, gs, bits))
+    return qmvd_config(M, N, K, gs, bits);
   if (f != '3' && f != '1' && qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits);
   if (f != '3' && qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
   return qmv32_config(M, N, K, gs, bits, true);
 }
 
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
+  if (c.kind == 4) return qmvp_launch(stream, c, p, bits, gs, grid_x);
+  if (c.kind == 3) return qmvd_launch(stream, c, p, bits, gs, grid_x);
   if (c.kind == 2) return qmvt_launch(stream, c, p, bits, gs, grid_x);
   return c.kind == 1 ? qmv16_launch(stream, c, p, bits, gs, grid_x) : qmv32_launch(stream, c, p, bits, gs, grid_x);
 }
 
 int qmv_lds_bytes_for(const QmvConfig& c, int gs, int M, int bits) {
+  if (c.kind == 4) return 0;
+  if (c.kind == 3) return qmvd_lds_bytes(c, M);
   if (c.kind == 2) return qmvt_lds_bytes(c, gs, M, bits);
   return c.kind == 1 ? qmv16_lds_bytes(c.slab_groups, gs, M, c.MQ, bits, c.NW)
                      : qmv32_lds_bytes(c.slab_groups, gs, M, c.MQ, bits, c.NW);

@@ -1,0 +1,364 @@
+// Decode matvec (qmv), one row of x, persistent pipelined kernel (gfx950).
+//
+// Arithmetic contract: the reference qmv (affine_qmv_fast / qmv_wide,
+// crates/lisa-mlx/src/shaders/common/matmul/quantized.metal:767-830,
+// 996-1088, qdot :196-295): per group y += scale*sum(x*q) + bias*sum(x) in
+// f32, weights never rounded, one bf16 rounding at the end.
+//
+// Shape of the kernel.  Every wave owns whole rows of W: lane l handles the
+// 32-code chunks l, l+64, l+128 of a row (J passes), so one load instruction
+// reads 64 consecutive chunks of one row (1 KB at 4 bits) and the lane's x
+// values (paired in unpack order, with their sums) stay in registers for the
+// whole launch.  A fixed grid of waves walks the rows (row = wave id + k *
+// number of waves) through a D-deep register ring: the loads of row k+D-1 are
+// issued before row k is computed, so every wave keeps D-1 rows in flight
+// while it computes.  All memory operations are buffer operations: rows past
+// the end and chunks past the row read as zero and stores past the end are
+// dropped by the hardware range check, so the loop body has no branches and
+// the compiler's waits are exact counts.  A row is finished with a fixed
+// butterfly over the 64 lanes (DPP within rows of 16 lanes, then lane swaps).
+// Codes become bf16 128+q with one v_and_or_b32 per pair (mantissa OR,
+// exact); v_dot2c_f32_bf16 forms sum(x*(128+q)) and the epilogue subtracts
+// 128*sum(x).  2-bit codes use masks 3/0xC/0x30 with x pre-scaled by
+// 1, 1/4, 1/16 (powers of two: exact).
+#include "lisaq_common.h"
+#include "qmv.h"
+
+#include <cstdlib>
+
+// experiment builds: compile-time switches that skip phases (never shipped)
+#ifndef QMVP_DBG
+#define QMVP_DBG 0
+#endif
+#define PDBG(bit) (QMVP_DBG & (bit))
+
+namespace lisaq {
+
+namespace {
+
+typedef __bf16 bf16x2p __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float pdot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2p, a), __builtin_bit_cast(bf16x2p, b), c,
+                                         false);
+}
+
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
+constexpr uint32_t kOob = 0x40000000u;  // past every buffer's range; two of them still fit in 32 bits
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+struct PConst {
+  uint32_t magic, m4, m2a, m2b, m2c;
+  __device__ __forceinline__ void init() {
+    magic = 0x43004300u;
+    m4 = 0x000F000Fu;
+    m2a = 0x00030003u;
+    m2b = 0x000C000Cu;
+    m2c = 0x00300030u;
+    // opaque to the optimizer: every (w & mask) | magic selects one v_and_or_b32
+    asm volatile("" : "+v"(magic));
+    asm volatile("" : "+s"(m4), "+s"(m2a), "+s"(m2b), "+s"(m2c));
+  }
+};
+
+// Pairs of one word, each a bf16x2.  4 bits: pair j = (code j, code j+4) as
+// 128+q.  2 bits: pair j = (code j, code j+8) as 128+f*q, f = 1, 4, 16 for
+// j % 3 = 0, 1, 2.
+template <int BITS>
+__device__ __forceinline__ void punpack(uint32_t w, const PConst& k, uint32_t* r) {
+  if constexpr (BITS == 4) {
+    r[0] = (w & k.m4) | k.magic;
+    r[1] = ((w >> 4) & k.m4) | k.magic;
+    r[2] = ((w >> 8) & k.m4) | k.magic;
+    r[3] = ((w >> 12) & k.m4) | k.magic;
+  } else {
+    const uint32_t s1 = w >> 6, s2 = w >> 12;
+    r[0] = (w & k.m2a) | k.magic;
+    r[1] = (w & k.m2b) | k.magic;
+    r[2] = (w & k.m2c) | k.magic;
+    r[3] = (s1 & k.m2a) | k.magic;
+    r[4] = (s1 & k.m2b) | k.magic;
+    r[5] = (s1 & k.m2c) | k.magic;
+    r[6] = (s2 & k.m2a) | k.magic;
+    r[7] = (s2 & k.m2b) | k.magic;
+  }
+}
+
+// Sum over the 64 lanes in a fixed order, all within the VALU (DPP): pair,
+// quad, half-row and row sums, then row_bcast15 / row_bcast31 carry rows
+// 0..2 into lane 63, which holds the total.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp_f<0x140, 0xF>(v);  // row_mirror: every lane of a row holds the row sum
+  v += dpp_f<0x142, 0xA>(v);  // row_bcast15: rows 1, 3 add the previous row
+  v += dpp_f<0x143, 0xC>(v);  // row_bcast31: rows 2, 3 add lane 31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+}  // namespace
+
+template <int BITS, int GS, int J, int D, int SBW>
+__global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
+  // SBW: bytes per lane of the two loads that bring a row's scales and
+  // biases (lanes [0, SBL)); they pass through LDS to the lanes that use them
+  typedef uint32_t sbv_t __attribute__((ext_vector_type(SBW >= 4 ? SBW / 4 : 1)));
+  constexpr int CB = BITS == 4 ? 16 : 8;  // chunk bytes: 32 codes either way
+  constexpr int WPC = CB / 4;
+  constexpr int PPW = 16 / BITS;
+  constexpr int NP = WPC * PPW;  // pairs per chunk (16)
+  static_assert(GS >= 32, "a chunk must lie inside one group");
+  typedef uint32_t chunk_t __attribute__((ext_vector_type(WPC)));
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gw = blockIdx.x * (blockDim.x >> 6) + wave;  // wave-uniform (row bases live in SGPRs)
+  const int nwv = gridDim.x * (blockDim.x >> 6);
+  const int N = p.N, C = p.chunks, G = p.G;
+  const uint32_t rowbytes = (uint32_t)C * CB;
+  const int cnt = gw < N ? (N - 1 - gw) / nwv + 1 : 0;  // rows of this wave
+  extern __shared__ float lds_res[];
+  float* res = lds_res + wave * p.tile_rows;  // p.tile_rows >= cnt
+  const int G2 = (2 * G + 15) & ~15;          // bytes of one staged s (or b) row, padded
+  unsigned char* sbl = reinterpret_cast<unsigned char*>(lds_res + (blockDim.x >> 6) * p.tile_rows) + wave * 2 * G2;
+  const int SBL = (2 * G + SBW - 1) / SBW;    // lanes that load
+  const bool sb_lane = lane < SBL;
+  const uint32_t sb_off = (uint32_t)lane * SBW;
+  unsigned char* sb_dst = sbl + sb_off;
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)p.K * 2);
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y, (uint32_t)N * 2);
+
+  // --- x of the lane's chunks (issued first; paired after the first rows are in flight)
+  uint32_t woff[J];  // byte offset of the chunk in a row
+  int gofs[J];       // byte offset of its group's scale in a staged row (0 past the row)
+  uint32_t raw[J][16];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    const bool ok = c < C;
+    woff[j] = ok ? (uint32_t)c * CB : kOob;
+    gofs[j] = ok ? (c * 32 / GS) * 2 : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (ok && !PDBG(32)) ? (uint32_t)c * 64 + 16 * i : kOob, 0, 0));
+      raw[j][4 * i] = v[0];
+      raw[j][4 * i + 1] = v[1];
+      raw[j][4 * i + 2] = v[2];
+      raw[j][4 * i + 3] = v[3];
+    }
+  }
+
+  // --- ring of D rows in flight
+  chunk_t wv[D][J];
+  sbv_t sv[D], bv[D];
+  // Each row gets its own buffer descriptors (scalar work): the lane offsets
+  // never change, and a row past the end has an empty range (reads zero).
+  auto issue = [&](int slot, int k) {
+    const bool ok = k < cnt;
+    const int64_t row = ok ? gw + (int64_t)k * nwv : 0;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(reinterpret_cast<const unsigned char*>(p.w) + row * rowbytes,
+                                                (ok && !PDBG(8)) ? rowbytes : 0);  // (8: skip the weight loads)
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s + row * G, ok ? 2 * G : 0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + row * G, ok ? 2 * G : 0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if constexpr (WPC == 4)
+        wv[slot][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b128(rw, woff[j], 0, 0));
+      else
+        wv[slot][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b64(rw, woff[j], 0, 0));
+    }
+    const uint32_t o = (sb_lane && !PDBG(1)) ? sb_off : kOob;  // (1: skip the scale/bias loads)
+    static_assert(SBW == 16 || SBW == 4, "scale/bias load width");
+    if constexpr (SBW == 16) {
+      sv[slot] = __builtin_bit_cast(sbv_t, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0));
+      bv[slot] = __builtin_bit_cast(sbv_t, __builtin_amdgcn_raw_buffer_load_b128(rb, o, 0, 0));
+    } else {
+      sv[slot] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
+      bv[slot] = __builtin_amdgcn_raw_buffer_load_b32(rb, o, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) issue(d, d);
+
+  // --- x paired in unpack order, with sums
+  uint32_t xp[J][NP];
+  float sx[J], st[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    auto xval = [&](int k) -> uint32_t { return (k & 1) ? (raw[j][k >> 1] >> 16) : (raw[j][k >> 1] & 0xffffu); };
+    sx[j] = 0.f;
+    st[j] = 0.f;
+#pragma unroll
+    for (int wd = 0; wd < WPC; ++wd)
+#pragma unroll
+      for (int q = 0; q < PPW; ++q) {
+        uint32_t lo, hi;
+        if constexpr (BITS == 4) {
+          lo = xval(8 * wd + q);
+          hi = xval(8 * wd + q + 4);
+          sx[j] += __uint_as_float(lo << 16) + __uint_as_float(hi << 16);
+        } else {
+          const int fq = q % 3;
+          const float f = fq == 0 ? 1.0f : (fq == 1 ? 0.25f : 0.0625f);
+          const float a = __uint_as_float(xval(16 * wd + q) << 16);
+          const float b = __uint_as_float(xval(16 * wd + q + 8) << 16);
+          sx[j] += a + b;
+          const float as = a * f, bs = b * f;  // power of two: exact
+          st[j] += as + bs;
+          lo = __float_as_uint(as) >> 16;
+          hi = __float_as_uint(bs) >> 16;
+        }
+        xp[j][wd * PPW + q] = lo | (hi << 16);
+      }
+    if constexpr (BITS == 4) st[j] = sx[j];
+  }
+
+  PConst kc;
+  kc.init();
+  auto compute = [&](int slot, int k) {
+    // this row's scales and biases -> the wave's LDS rows (in-order per wave)
+    if (sb_lane) {
+      *reinterpret_cast<sbv_t*>(sb_dst) = sv[slot];
+      *reinterpret_cast<sbv_t*>(sb_dst + G2) = bv[slot];
+    }
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+      for (int wd = 0; wd < WPC; ++wd) {
+        if (PDBG(2)) {  // skip the arithmetic
+          d0 += __uint_as_float(wv[slot][j][wd] & 0x3fffffu);
+          continue;
+        }
+        uint32_t r[PPW];
+        punpack<BITS>(wv[slot][j][wd], kc, r);
+#pragma unroll
+        for (int q = 0; q < PPW; ++q) {
+          if (q & 1) d1 = pdot2(r[q], xp[j][wd * PPW + q], d1);
+          else d0 = pdot2(r[q], xp[j][wd * PPW + q], d0);
+        }
+      }
+      const float s = bf2f(*reinterpret_cast<const uint16_t*>(sbl + gofs[j]));
+      const float b = bf2f(*reinterpret_cast<const uint16_t*>(sbl + G2 + gofs[j]));
+      part = fmaf(s, (d0 + d1) - 128.0f * st[j], fmaf(b, sx[j], part));
+    }
+    const float total = wave_sum(part);
+    // results wait in LDS: a store here would be a vector-memory event
+    // between the ring's loads and blur the compiler's exact wait counts
+    if (lane == 0 && k < cnt) res[k] = total;
+  };
+
+  for (int k0 = 0; k0 < cnt; k0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      issue((d + D - 1) % D, k0 + d + D - 1);
+      compute(d, k0 + d);
+    }
+  }
+  // (a wave's LDS operations complete in order: lane 0's writes are visible)
+  for (int k = lane; k < cnt; k += 64)
+    __builtin_amdgcn_raw_buffer_store_b16(f2bf(res[k]), ry, (uint32_t)(gw + k * nwv) * 2, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+  QmvConfig c{};
+  c.kind = -1;
+  if (M != 1 || (bits != 2 && bits != 4) || K % 32 != 0) return c;
+  if (!(bits == 4 ? (gs == 32 || gs == 64 || gs == 128) : (gs == 64 || gs == 128))) return c;
+  const int64_t C = K / 32;
+  if (C > 192) return c;
+  const int64_t rowbytes = C * (bits == 4 ? 16 : 8);
+  if (N * rowbytes >= (int64_t)kOob || N * (K / gs) * 2 >= (int64_t)kOob || K * 2 >= (int64_t)kOob) return c;
+  c.MR = 1;
+  c.U = (int)((C + 63) / 64);  // J passes
+  c.S = 2;                     // ring depth D
+  if (const char* env = getenv("LISAQ_QMVP_D")) {
+    const int v = atoi(env);
+    if (v == 2 || v == 3) c.S = v;
+  }
+  int wgs_per_cu = 2;
+  if (const char* env = getenv("LISAQ_QMVP_WG")) {
+    const int v = atoi(env);
+    if (v >= 1 && v <= 16) wgs_per_cu = v;
+  }
+  c.NW = 4;
+  int64_t grid = 256LL * wgs_per_cu;
+  const int64_t need = (N + 3) / 4;
+  c.tiles = (int)(grid < need ? grid : need);
+  const int64_t waves = 4LL * c.tiles;
+  c.tile_rows = (int)((N + waves - 1) / waves);  // rows per wave, at most
+  c.S_inner = (int)C;
+  // scale/bias row load width: the widest that divides the row and fits 64 lanes
+  const int64_t G = K / gs;
+  c.sbw = 0;
+  for (int w : {16, 4})
+    if ((2 * G) % w == 0 && (2 * G) / w <= 64) {
+      c.sbw = w;
+      break;
+    }
+  if (c.sbw == 0) return c;
+  const int64_t g2 = (2 * G + 15) & ~15;
+  c.lds_bytes = (int)(4 * 4 * c.tile_rows + 4 * 2 * g2);
+  if (c.lds_bytes > 64 * 1024) return c;  // (kind stays -1)
+  c.ws_bytes = 0;
+  c.kind = 4;
+  return c;
+}
+
+typedef void (*qmvp_fn)(QmvParams);
+
+template <int BITS, int GS, int J, int D>
+static qmvp_fn qmvp_pick_w(int w) {
+  if (w == 16) return qmvp_kernel<BITS, GS, J, D, 16>;
+  if (w == 4) return qmvp_kernel<BITS, GS, J, D, 4>;
+  return nullptr;
+}
+
+template <int BITS, int GS, int J>
+static qmvp_fn qmvp_pick_d(int d, int w) {
+  if (d == 2) return qmvp_pick_w<BITS, GS, J, 2>(w);
+  if (d == 3) return qmvp_pick_w<BITS, GS, J, 3>(w);
+  return nullptr;
+}
+
+template <int BITS, int GS>
+static qmvp_fn qmvp_pick(int j, int d, int w) {
+  if (j == 1) return qmvp_pick_d<BITS, GS, 1>(d, w);
+  if (j == 2) return qmvp_pick_d<BITS, GS, 2>(d, w);
+  if (j == 3) return qmvp_pick_d<BITS, GS, 3>(d, w);
+  return nullptr;
+}
+
+int qmvp_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
+  qmvp_fn fn = nullptr;
+  if (bits == 4 && gs == 64) fn = qmvp_pick<4, 64>(c.U, c.S, c.sbw);
+  else if (bits == 4 && gs == 32) fn = qmvp_pick<4, 32>(c.U, c.S, c.sbw);
+  else if (bits == 4 && gs == 128) fn = qmvp_pick<4, 128>(c.U, c.S, c.sbw);
+  else if (bits == 2 && gs == 64) fn = qmvp_pick<2, 64>(c.U, c.S, c.sbw);
+  else if (bits == 2 && gs == 128) fn = qmvp_pick<2, 128>(c.U, c.S, c.sbw);
+  if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmvp: bits=%d gs=%d J=%d D=%d", bits, gs, c.U, c.S);
+  if (p.M != 1 || p.tiles) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: one plain row only");
+  if (p.K / 32 != c.S_inner) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: configuration made for another K");
+  p.chunks = c.S_inner;
+  p.tile_rows = c.tile_rows;
+  if ((int64_t)grid_x * c.NW * c.tile_rows < p.N) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: grid too small");
+  hipLaunchKernelGGL(fn, dim3(grid_x), dim3(64 * c.NW), c.lds_bytes, stream, p);
+  return check_launch("qmvp");
+}
+
+}  // namespace lisaq

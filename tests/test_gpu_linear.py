@@ -56,6 +56,31 @@ def test_qmv_parity(dev, oracle, M, N, K, bits, gs):
         assert np.array_equal(got, got2)
 
 
+@pytest.mark.parametrize("kernel", ["p", "d", "t", "16", "32"])
+@pytest.mark.parametrize("M,N,K,bits,gs", [
+    (1, 100, 1024, 4, 64),      # fewer rows than waves (persistent kernel), J = 1
+    (1, 4099, 2560, 4, 64),     # J = 2, N tail
+    (1, 17408, 5120, 4, 64),    # north star, J = 3
+    (1, 3000, 5120, 2, 64),
+    (1, 1000, 4096, 4, 32),
+    (1, 1000, 6144, 4, 128),
+    (1, 777, 2048, 2, 128),
+    (2, 3001, 5120, 4, 64),
+    (2, 640, 2048, 2, 64),
+])
+def test_qmv_every_kernel(dev, oracle, monkeypatch, kernel, M, N, K, bits, gs):
+    """Each matvec kernel (forced through LISAQ_QMV_KERNEL; a shape it does not
+    take falls through to the next one) against the oracle."""
+    monkeypatch.setenv("LISAQ_QMV_KERNEL", kernel)
+    rng = np.random.default_rng(N * 3 + K + bits + gs + M)
+    w, s, b = np_linear(rng, N, K, bits, gs, s_std=0.02 if bits == 4 else 0.05,
+                        b_std=0.01 if bits == 4 else 0.02)
+    x = np_x(rng, M, K)
+    ref = oracle.qmv(x, w, s, b, gs, bits)
+    got = _run(ops.qmv, dev, x, w, s, b, gs, bits)
+    assert_close_bf16(got, ref, what=f"qmv[{kernel}] M={M} N={N} K={K} bits={bits} gs={gs}")
+
+
 @pytest.mark.parametrize("M,N,K,bits,gs", [
     (33, 256, 512, 4, 64), (64, 256, 1024, 4, 64), (130, 300, 512, 4, 64), (128, 512, 2048, 2, 64),
     (96, 256, 1024, 4, 32), (50, 256, 1024, 4, 128), (200, 1024, 768, 4, 64), (13, 256, 4096, 2, 128),
@@ -107,7 +132,7 @@ def test_north_star_qmv_shape(dev, oracle, bits):
 def test_serial_rows_bitwise_equal_to_single_rows(dev, bits):
     """array_ops.rs:650-710: batched rows == independent M=1 calls, bitwise."""
     rng = np.random.default_rng(99 + bits)
-    for N, K in ((64, 512), (2560, 9728), (9728, 2560)):
+    for N, K in ((64, 512), (2560, 9728), (9728, 2560), (17408, 5120)):
         w, s, b = np_linear(rng, N, K, bits, 64)
         x = np_x(rng, 3, K)
         batched = _run(ops.quantized_matmul_serial_rows, dev, x, w, s, b, 64, bits)
