@@ -20,6 +20,7 @@
 //    runs on the matrix cores.
 #include "lisaq_common.h"
 #include "qmm.h"
+#include <cstdlib>
 #include <type_traits>
 
 namespace lisaq {
@@ -62,14 +63,56 @@ struct MGeo {
 };
 
 constexpr int BK = 64;
-constexpr int XS = BK + 8;  // LDS row stride of the x tile (bf16), padded
+// x tile in LDS: rows of 64 bf16 (128 B) written by direct-to-LDS loads, one
+// wave instruction = 8 rows = 1 KB.  The 16-byte chunks of a row are XOR-
+// swizzled by (row % 8) and each 8-row group is followed by 16 bytes of
+// padding, so the A-operand reads (32 rows, one chunk each) hit distinct banks.
+constexpr int XG = 1024 + 16;  // bytes per 8-row group
+constexpr int NBUF = 3;        // LDS ring: step k+2 lands while step k runs
+
+__device__ __forceinline__ int x_lds_off(int row, int chunk) {
+  return (row >> 3) * XG + (row & 7) * 128 + ((chunk ^ (row & 7)) << 4);
+}
+
+// 16 / 4 / 2 bytes per lane from global memory straight into LDS (lane l
+// writes lds + size*l; lds must be wave-uniform).
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+__device__ __forceinline__ void load_lds2(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 2, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (expcnt, lgkmcnt left alone): the direct-to-LDS loads
+// are not tracked by the compiler's own waits.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+template <int BITS, int GS, int MT, int NT>
+struct QmmLds {
+  static constexpr int BM = 32 * MT, BN = 4 * 32 * NT;
+  static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
+  static constexpr int X = BM / 8 * XG;            // x tile
+  static constexpr int W = BN * RB;                // packed W tile
+  static constexpr int S = BN * 4;                 // scales: the aligned bf16 pair holding the step's group(s)
+  static constexpr int WSTAGE = W + 2 * S;         // packed W + scales + biases of one step
+  static constexpr int W0 = NBUF * X;              // W ring after the x ring
+  static constexpr int TOTAL = NBUF * (X + WSTAGE);
+};
 
 template <int BITS, int GS, int MT, int NT>
 __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
-  constexpr int BM = 32 * MT;
-  constexpr int BN = 4 * 32 * NT;
-  __shared__ __attribute__((aligned(16))) uint16_t xt[2][BM * XS];
+  using L = QmmLds<BITS, GS, MT, NT>;
+  constexpr int BM = L::BM;
+  constexpr int BN = L::BN;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -100,48 +143,93 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     m0 = blockIdx.y * BM;
   }
 
-  // W rows of this wave
-  const int64_t kq = p.K / G::PACK;
-  const uint32_t* wr[NT];
-  const uint16_t* sr[NT];
-  const uint16_t* br[NT];
+  // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
+  // matrix are clamped to the last one, their results are never stored)
+  // x: BM/8 instructions of 1 KB, XI per wave; lane l fills row 8g + l/8,
+  // physical chunk l%8 (= logical chunk (l%8) ^ (row%8))
+  constexpr int XI = BM / 8 / 4;
+  uint32_t xoff[XI];  // element offsets (the host checks x fits 2^31 elements)
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    int n = nt0 + (wave * NT + nt) * 32 + col;
-    n = n < p.N ? n : p.N - 1;
-    wr[nt] = w + (int64_t)n * kq + h * G::WPL;
-    sr[nt] = sc + (int64_t)n * p.G;
-    br[nt] = bi + (int64_t)n * p.G;
+  for (int i = 0; i < XI; ++i) {
+    const int r = (wave * XI + i) * 8 + (lane >> 3);
+    int row = m0 + r;
+    row = row < M ? row : M - 1;
+    xoff[i] = (uint32_t)row * (uint32_t)p.K + (uint32_t)(((lane & 7) ^ (r & 7)) << 3);
   }
+  // W: BN rows x RB bytes, row-major; 16 bytes per lane, WI instructions per wave
+  constexpr int WLPR = L::RB / 16;             // lanes per row
+  constexpr int WI = L::W / 1024 / 4;          // instructions per wave
+  static_assert(WI >= 1 && L::W % 4096 == 0, "W tile geometry");
+  const unsigned char* wsrc[WI];
+  const int64_t rowbytes = (int64_t)p.K * BITS / 8;
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int r = (wave * WI + i) * (64 / WLPR) + lane / WLPR;
+    int n = nt0 + r;
+    n = n < p.N ? n : p.N - 1;
+    wsrc[i] = reinterpret_cast<const unsigned char*>(w) + n * rowbytes + (lane % WLPR) * 16;
+  }
+  // scales / biases: per row the 4-byte-aligned bf16 pair holding the step's
+  // group(s); 64 rows per instruction (BN/64 instructions per array, spread
+  // over the waves)
+  constexpr int SI = BN / 64;                  // instructions per array
+  static_assert(SI % 4 == 0 || SI == 2, "scale tile geometry");
 
-  // x tile loader: BM rows x 64 bf16 = BM*8 uint4, 256 threads
-  constexpr int XV = BM * 8 / 256;
-  auto load_x = [&](int k0, u32x4* v) {
+  constexpr int SBI = (SI * 2 + 3) / 4;         // scale/bias instructions per wave
+  constexpr int VM_X = XI, VM_W = WI + SBI;    // DMA instructions per wave: x tile, W stage
+  auto issue_x = [&](int k, int stage) {
+    unsigned char* st = smem + stage * L::X;
+    const int k0 = k * BK;
 #pragma unroll
-    for (int i = 0; i < XV; ++i) {
-      const int idx = threadIdx.x + i * 256;
-      const int r = idx >> 3, c8 = idx & 7;
-      int row = m0 + r;
-      row = row < M ? row : M - 1;
-      v[i] = *reinterpret_cast<const u32x4*>(x + (int64_t)row * p.K + k0 + c8 * 8);
+    for (int i = 0; i < XI; ++i) load_lds16(x + xoff[i] + k0, st + (wave * XI + i) * XG);
+  };
+  auto issue_w = [&](int k, int stage) {
+    unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
+    const int k0 = k * BK;
+#pragma unroll
+    for (int i = 0; i < WI; ++i) load_lds16(wsrc[i] + (int64_t)k0 * BITS / 8, st + (wave * WI + i) * 1024);
+    // 2*SI scale/bias instructions over the 4 waves
+    const int g = k0 / GS;
+#pragma unroll
+    for (int i = 0; i < SBI; ++i) {
+      const int idx = wave + 4 * i;  // 0 .. 2*SI-1: s row blocks, then b row blocks
+      const bool is_b = idx >= SI;
+      const int blk = is_b ? idx - SI : idx;
+      // (lanes of this instruction load rows blk*64 + lane)
+      const int64_t roff = (int64_t)(nt0 + blk * 64 + lane < p.N ? nt0 + blk * 64 + lane : p.N - 1) * p.G + g;
+      const uint16_t* src = (is_b ? bi : sc) + (roff & ~(int64_t)1);  // (G is even: 4-byte aligned)
+      load_lds4(src, st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
     }
   };
-  auto store_x = [&](int buf, const u32x4* v) {
-#pragma unroll
-    for (int i = 0; i < XV; ++i) {
-      const int idx = threadIdx.x + i * 256;
-      const int r = idx >> 3, c8 = idx & 7;
-      *reinterpret_cast<u32x4*>(&xt[buf][r * XS + c8 * 8]) = v[i];
-    }
-  };
+
+  // ---- one K-step's W of this lane (LDS stage): packed words, scale, bias
   typedef typename std::conditional<G::WPL == 4, u32x4, u32x2>::type WV;
-  auto load_w = [&](int k0, WV* wv, float* s, float* b) {
-    const int g = (k0 + 32 * h) / GS;
+  struct WLane {
+    WV w[NT];
+    float s[NT], b[NT];
+  };
+  auto read_w = [&](int k, int stage, WLane& o) {
+    const unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
+    const int g0 = k * BK / GS;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      wv[nt] = *reinterpret_cast<const WV*>(wr[nt] + (int64_t)k0 / G::PACK);
-      s[nt] = bf2f(sr[nt][g]);
-      b[nt] = bf2f(br[nt][g]);
+      const int r = (wave * NT + nt) * 32 + col;
+      // half of the staged pair: the lane's group (gs 32: the step's two
+      // groups, pair-aligned since G is even; else the element's parity)
+      const int n = nt0 + r < p.N ? nt0 + r : p.N - 1;
+      const int half = GS == 32 ? h : (int)(((int64_t)n * p.G + g0) & 1);
+      const int si = r * 4 + half * 2;
+      o.s[nt] = bf2f(*reinterpret_cast<const uint16_t*>(st + L::W + si));
+      o.b[nt] = bf2f(*reinterpret_cast<const uint16_t*>(st + L::W + L::S + si));
+      o.w[nt] = *reinterpret_cast<const WV*>(st + r * L::RB + h * (4 * G::WPL));
+    }
+  };
+  // dequantize word jw into the B operands [nt][16] bf16x2
+  auto dequant_word = [&](const WLane& r, int jw, uint32_t (*bop)[16]) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (BITS == 4) deq4(r.w[nt][jw], r.s[nt], r.b[nt], &bop[nt][jw * 4]);
+      else deq2(r.w[nt][jw], r.s[nt], r.b[nt], &bop[nt][jw * 8]);
     }
   };
 
@@ -151,57 +239,57 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x16{};
 
+  // Pipeline.  Step k reads x stage k % 3 and refills, sub-step by sub-step,
+  // the B operands with step k+1's W (W stage (k+1) % 3, landed a step
+  // earlier); meanwhile the copies of x(k+2) and W(k+3) are in flight.  Copies
+  // past the last step re-read it, so every step issues the same number of
+  // copies and the waits are constants.
   const int nk = p.K / BK;
-  u32x4 xv[XV];
-  WV wv[NT];
-  float sv[NT], bv[NT];
-  load_x(0, xv);
-  load_w(0, wv, sv, bv);
-  store_x(0, xv);
+  auto kc = [&](int k) { return k < nk ? k : nk - 1; };
+  uint32_t bop[NT][16];
+  issue_x(0, 0);
+  issue_w(0, 0);
+  issue_w(kc(1), 1);
+  issue_x(kc(1), 1);
+  issue_w(kc(2), 2);
+  wait_vm<VM_X + VM_W>();  // x(0), W(0), W(1) landed (this wave's part)
   __syncthreads();
+  {
+    WLane w0;
+    read_w(0, 0, w0);
+#pragma unroll
+    for (int jw = 0; jw < G::WPL; ++jw) dequant_word(w0, jw, bop);
+  }
 
+  int xs = 0, ws1 = 1;  // x stage of step k, W stage of step k+1
   for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nk;
-    WV wn[NT];
-    float sn[NT], bn[NT];
-    if (more) {
-      load_x((kt + 1) * BK, xv);
-      load_w((kt + 1) * BK, wn, sn, bn);
-    }
-    // dequantize this K-step's W into B operands: [nt][j] bf16x8
-    uint32_t bop[NT][16];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-#pragma unroll
-      for (int jw = 0; jw < G::WPL; ++jw) {
-        if (BITS == 4) deq4(wv[nt][jw], sv[nt], bv[nt], &bop[nt][jw * 4]);
-        else deq2(wv[nt][jw], sv[nt], bv[nt], &bop[nt][jw * 8]);
-      }
-    }
-    const uint16_t* xa = &xt[buf][col * XS + 32 * h];
+    const int xs2 = xs == 0 ? 2 : xs - 1;    // (k+2) % 3
+    const int ws3 = ws1 == 0 ? 2 : ws1 - 1;  // (k+3) % 3 = k % 3
+    issue_x(kc(kt + 2), xs2);
+    issue_w(kc(kt + 3), ws3);
+    WLane wn;
+    read_w(kc(kt + 1), ws1, wn);
+    const unsigned char* xb = smem + xs * L::X;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       u32x4 a[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) a[mt] = *reinterpret_cast<const u32x4*>(xa + mt * 32 * XS + 8 * j);
+      for (int mt = 0; mt < MT; ++mt)
+        a[mt] = *reinterpret_cast<const u32x4*>(xb + x_lds_off(mt * 32 + col, 4 * h + j));
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const u32x4 bw = u32x4{bop[nt][4 * j], bop[nt][4 * j + 1], bop[nt][4 * j + 2], bop[nt][4 * j + 3]};
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma32x32x16(as_bf16x8(a[mt]), as_bf16x8(bw), acc[mt][nt]);
       }
+      // the B operands of j are consumed: refill them from the next step's word
+      constexpr int JPW = 4 / G::WPL;  // K sub-steps per word
+      if ((j + 1) % JPW == 0) dequant_word(wn, (j + 1) / JPW - 1, bop);
     }
-    if (more) {
-      store_x(buf ^ 1, xv);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        wv[nt] = wn[nt];
-        sv[nt] = sn[nt];
-        bv[nt] = bn[nt];
-      }
-    }
-    __syncthreads();
+    wait_vm<VM_X + VM_W>();  // x(k+1), W(k+2) landed (issued one step ago)
+    __syncthreads();         // ... for every wave; stages of step k are free
+    xs = xs == 2 ? 0 : xs + 1;
+    ws1 = ws1 == 2 ? 0 : ws1 + 1;
   }
 
   // epilogue: D[m][n], lane holds n = col, rows 8*(i/4) + 4*h + (i%4)
@@ -222,7 +310,11 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
 // ---------------------------------------------------------------------------
 QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   QmmConfig c{};
-  c.MT = 4;
+  c.MT = M > 128 ? 8 : 4;
+  if (const char* env = getenv("LISAQ_QMM_MT")) {
+    const int v = atoi(env);
+    if (v == 4 || v == 8) c.MT = v;
+  }
   c.NT = 2;
   c.BM = 32 * c.MT;
   c.BN = 128 * c.NT;
@@ -236,22 +328,38 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
 
 typedef void (*qmm_fn)(QmmParams);
 
+static int qmm_lds_bytes(int MT, int bits, int gs) {
+  auto pick = [&](auto l) { return decltype(l)::TOTAL; };
+  if (MT == 8) {
+    if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 8, 2>{}) : pick(QmmLds<4, 64, 8, 2>{});
+    return gs == 32 ? pick(QmmLds<2, 32, 8, 2>{}) : pick(QmmLds<2, 64, 8, 2>{});
+  }
+  if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 4, 2>{}) : pick(QmmLds<4, 64, 4, 2>{});
+  return gs == 32 ? pick(QmmLds<2, 32, 4, 2>{}) : pick(QmmLds<2, 64, 4, 2>{});
+}
+
+template <int MT>
 static qmm_fn qmm_kernel_for(int bits, int gs) {
-  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, 4, 2>;
-  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, 4, 2>;
-  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, 4, 2>;
-  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, 4, 2>;
-  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, 4, 2>;
-  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, 4, 2>;
+  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, MT, 2>;
+  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, MT, 2>;
+  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, MT, 2>;
+  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, MT, 2>;
+  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, MT, 2>;
+  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, MT, 2>;
   return nullptr;
 }
 
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
                int grid_y) {
-  qmm_fn fn = qmm_kernel_for(bits, gs);
+  qmm_fn fn = c.MT == 8 ? qmm_kernel_for<8>(bits, gs) : qmm_kernel_for<4>(bits, gs);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);
-  (void)c;
-  hipLaunchKernelGGL(fn, dim3(grid_x, grid_y), dim3(256), 0, stream, p);
+  const int lds = qmm_lds_bytes(c.MT, bits, gs);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmm: LDS %d bytes: %s", lds, hipGetErrorString(e));
+  }
+  LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
+  hipLaunchKernelGGL(fn, dim3(grid_x, grid_y), dim3(256), lds, stream, p);
   return check_launch("qmm");
 }
 
