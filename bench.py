@@ -31,6 +31,15 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "4-bit qmv GB/s (% HBM peak) @M=1; qmm TFLOP/s (% bf16 MFMA peak) @M=2048"
 
 
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload, each
+# scaled by the counter's reading for a 64 MiB device copy (see the profiles/ summaries for the
+# commands and raw counts).
+QMV_TRAFFIC_BYTES = round((24566.0 * 1.9993 + 136.0) * 1024)
+QMM_TRAFFIC_BYTES = round((218411.6 * 1.9993 + 86364.3) * 1024)
+QMV_KERNEL = "lisaq::qmvp_kernel<4, 64, 3, 2, 16>"
+QMM_KERNEL = "lisaq::qmm_kernel<4, 64, 8, 2>"
+
+
 def qmv_bytes(M, N, K, bits=4, gs=64):
     return N * K * bits // 8 + 2 * 2 * N * (K // gs) + 2 * M * K + 2 * M * N
 
@@ -44,6 +53,9 @@ def main():
     ap.add_argument("--sets", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-qmm", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only run a plain 64 MiB device copy (the reference kernel for the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
@@ -56,6 +68,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": src.numel(), "bytes_written": dst.numel(),
+                          "calls": 20}), flush=True)
+        return
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x5EED + 1)
     M, N, K, bits, gs = 1, 17408, 5120, 4, 64
@@ -105,10 +126,12 @@ def main():
 
     # --- qmm: prefill M=2048 (eager; each call is ~0.3-1 ms) -------------------
     Mq = 2048
+    if args.no_qmm:
+        args.qmm_steps = 0
     wq = sets[0]
     xq = torch_x(Mq, K, device=dev, generator=gen)
     with torch.cuda.stream(stream):
-        for _ in range(3):
+        for _ in range(3 if args.qmm_steps else 0):
             ops.quantized_matmul(xq, *wq, True, gs, bits)
     torch.cuda.synchronize()
     q0 = torch.cuda.Event(enable_timing=True)
@@ -119,7 +142,7 @@ def main():
             ops.quantized_matmul(xq, *wq, True, gs, bits)
         q1.record(stream)
     torch.cuda.synchronize()
-    qmm_s = q0.elapsed_time(q1) * 1e-3 / args.qmm_steps
+    qmm_s = q0.elapsed_time(q1) * 1e-3 / max(args.qmm_steps, 1)
     flops = 2.0 * Mq * N * K
     tflops = flops / qmm_s / 1e12
 
@@ -149,15 +172,16 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "lisaq::qmv_kernel<4,64,1,4>", "bytes_per_launch": nbytes,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": QMV_TRAFFIC_BYTES,
+            "kernel": QMV_KERNEL, "bytes_per_launch": nbytes,
             "avg_launch_us": round(per_step_s * 1e6, 3),
         },
         "qmm": {
             "workload": "qmm 4-bit gs64 M=2048 K=5120 N=17408 (prefill)",
             "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_call": round(qmm_s * 1e3, 4),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+                         "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         "traffic": QMM_TRAFFIC_BYTES, "kernel": QMM_KERNEL},
         },
         "cpu_baseline": cpu,
     }

@@ -97,7 +97,7 @@ static int run_qmm(hipStream_t st, const void* x, const uint32_t* w, const void*
   p.N = (int)N;
   p.K = (int)K;
   p.G = (int)(K / gs);
-  return qmm_launch(st, c, p, bits, gs, c.grid_n, c.grid_m);
+  return qmm_launch(st, c, p, bits, gs, c.grid, 1);
 }
 
 // Gather workspace layout: [counts 256 B][qmv table][qmm table], 256-B aligned.

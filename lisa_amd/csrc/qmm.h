@@ -16,6 +16,7 @@ struct QmmParams {
 
 struct QmmConfig {
   int MT, NT, BM, BN, grid_n, grid_m;
+  int grid;  // workgroups of a plain (no tile table) launch: grid_n * grid_m
 };
 
 QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits);

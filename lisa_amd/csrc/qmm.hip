@@ -32,14 +32,26 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Byte i of a word as f32 (v_cvt_f32_ubyte<i>: one instruction; written out
+// because the compiler turns masked nibble fields into v_bfe + ubyte0).
+template <int I>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  float r;
+  if constexpr (I == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (I == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (I == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
 // Dequantize the 8 codes of one u32 (4-bit) into 4 bf16x2 in natural K order.
 __device__ __forceinline__ void deq4(uint32_t w, float s, float b, uint32_t* o) {
   const uint32_t lo = w & 0x0F0F0F0Fu;         // codes 0,2,4,6
   const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
-  o[0] = pk_bf16(fmaf(s, (float)(lo & 0xff), b), fmaf(s, (float)(hi & 0xff), b));
-  o[1] = pk_bf16(fmaf(s, (float)((lo >> 8) & 0xff), b), fmaf(s, (float)((hi >> 8) & 0xff), b));
-  o[2] = pk_bf16(fmaf(s, (float)((lo >> 16) & 0xff), b), fmaf(s, (float)((hi >> 16) & 0xff), b));
-  o[3] = pk_bf16(fmaf(s, (float)(lo >> 24), b), fmaf(s, (float)(hi >> 24), b));
+  o[0] = pk_bf16(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
+  o[1] = pk_bf16(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
+  o[2] = pk_bf16(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
+  o[3] = pk_bf16(fmaf(s, ubyte_f32<3>(lo), b), fmaf(s, ubyte_f32<3>(hi), b));
 }
 
 // Dequantize the 16 codes of one u32 (2-bit) into 8 bf16x2 in natural K order.
@@ -48,12 +60,14 @@ __device__ __forceinline__ void deq2(uint32_t w, float s, float b, uint32_t* o) 
   const uint32_t c1 = (w >> 2) & 0x03030303u;  // codes 1,5,9,13
   const uint32_t c2 = (w >> 4) & 0x03030303u;  // codes 2,6,10,14
   const uint32_t c3 = (w >> 6) & 0x03030303u;  // codes 3,7,11,15
-#pragma unroll
-  for (int byte = 0; byte < 4; ++byte) {
-    const int sh = 8 * byte;
-    o[2 * byte + 0] = pk_bf16(fmaf(s, (float)((c0 >> sh) & 0xff), b), fmaf(s, (float)((c1 >> sh) & 0xff), b));
-    o[2 * byte + 1] = pk_bf16(fmaf(s, (float)((c2 >> sh) & 0xff), b), fmaf(s, (float)((c3 >> sh) & 0xff), b));
-  }
+  o[0] = pk_bf16(fmaf(s, ubyte_f32<0>(c0), b), fmaf(s, ubyte_f32<0>(c1), b));
+  o[1] = pk_bf16(fmaf(s, ubyte_f32<0>(c2), b), fmaf(s, ubyte_f32<0>(c3), b));
+  o[2] = pk_bf16(fmaf(s, ubyte_f32<1>(c0), b), fmaf(s, ubyte_f32<1>(c1), b));
+  o[3] = pk_bf16(fmaf(s, ubyte_f32<1>(c2), b), fmaf(s, ubyte_f32<1>(c3), b));
+  o[4] = pk_bf16(fmaf(s, ubyte_f32<2>(c0), b), fmaf(s, ubyte_f32<2>(c1), b));
+  o[5] = pk_bf16(fmaf(s, ubyte_f32<2>(c2), b), fmaf(s, ubyte_f32<2>(c3), b));
+  o[6] = pk_bf16(fmaf(s, ubyte_f32<3>(c0), b), fmaf(s, ubyte_f32<3>(c1), b));
+  o[7] = pk_bf16(fmaf(s, ubyte_f32<3>(c2), b), fmaf(s, ubyte_f32<3>(c3), b));
 }
 
 template <int BITS>
@@ -139,8 +153,10 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     m0 = 0;
     nt0 = t.w * BN;
   } else {
-    nt0 = blockIdx.x * BN;
-    m0 = blockIdx.y * BM;
+    // row-block major: consecutive workgroups share an x row block and walk W
+    const int gn = (p.N + BN - 1) / BN;
+    nt0 = (blockIdx.x % gn) * BN;
+    m0 = (blockIdx.x / gn) * BM;
   }
 
   // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
@@ -320,6 +336,7 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   c.BN = 128 * c.NT;
   c.grid_n = (int)((N + c.BN - 1) / c.BN);
   c.grid_m = (int)((M + c.BM - 1) / c.BM);
+  c.grid = c.grid_n * c.grid_m;  // 1-D launch (see the kernel's tile order)
   (void)K;
   (void)gs;
   (void)bits;
