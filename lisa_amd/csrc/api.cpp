@@ -347,7 +347,7 @@ int lisaq_gather_qmm(void* stream, const void* x, const uint32_t* w, const void*
   int32_t* counts = (int32_t*)base;
   int4* qmv_tab = (int4*)(base + L.qmv_off);
   int4* qmm_tab = (int4*)(base + L.qmm_off);
-  rc = launch_tile_table(st, rhs, R, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN, qmv_tab, L.qmv_cap, qmm_tab,
+  rc = launch_tile_table(st, rhs, R, E, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN, qmv_tab, L.qmv_cap, qmm_tab,
                          L.qmm_cap, counts);
   if (rc) return rc;
   if (L.qmv_cap > 0) {

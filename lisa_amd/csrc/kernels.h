@@ -17,7 +17,8 @@ int launch_gather_rows(hipStream_t st, const uint16_t* x, const int32_t* rows, u
 int launch_swiglu(hipStream_t st, const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n);
 int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const int32_t* inv,
                    uint16_t* out, int64_t T, int k, int64_t H);
-int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int N, int limit, int VR, int BM, int BN,
+constexpr int kTileTableMaxExperts = 16384;
+int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int E, int N, int limit, int VR, int BM, int BN,
                       int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap, int32_t* counts);
 
 }  // namespace lisaq

@@ -32,8 +32,9 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     v[i] = e < E ? l[e] : -INFINITY;
     if (e >= E) taken |= 1u << i;
   }
-  float sel[32];
-  int sid[32];
+  // lane r keeps round r's winner (k <= 64), so nothing lives in scratch
+  float mysel = -INFINITY;
+  int mysid = 0;
   for (int r = 0; r < k; ++r) {
     float best = 0.f;
     int bi = 0x7fffffff;
@@ -57,22 +58,26 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
       }
     }
     if ((bi & 63) == lane && bi != 0x7fffffff) taken |= 1u << (bi >> 6);
-    sel[r] = best;
-    sid[r] = bi;
+    if (lane == r) {
+      mysel = best;
+      mysid = bi;
+    }
   }
-  if (lane == 0) {
-    float mx = sel[0];
-    for (int r = 1; r < k; ++r) mx = (mx < sel[r]) ? sel[r] : mx;
-    float ex[32], sum = 0.f;
-    for (int r = 0; r < k; ++r) {
-      ex[r] = expf(sel[r] - mx);
-      sum += ex[r];
-    }
-    const float inv = 1.0f / sum;
-    for (int r = 0; r < k; ++r) {
-      idx[t * k + r] = sid[r];
-      wts[t * k + r] = ex[r] * inv;
-    }
+  // softmax over the k selected logits: max, then exp and the sum in round
+  // order (lane 0 adds lanes 1..k-1 in turn), w = e * (1/sum)
+  float mx = mysel;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = __shfl_xor(mx, off);
+    mx = mx < o ? o : mx;
+  }
+  const float ex = lane < k ? expf(mysel - mx) : 0.f;
+  float sum = 0.f;
+  for (int r = 0; r < k; ++r) sum += __shfl(ex, r);
+  const float inv = 1.0f / sum;
+  if (lane < k) {
+    idx[t * k + lane] = mysid;
+    wts[t * k + lane] = ex * inv;
   }
 }
 
@@ -227,9 +232,32 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
   out[i] = f2bf(__fmul_rn(silu_bf16(bf2f(g[i])), bf2f(u[i])));
 }
 
+// 8 elements per thread (16-byte loads and stores); n % 8 == 0, 16-byte aligned
+__global__ __launch_bounds__(256) void swiglu8_kernel(const u32x4* __restrict__ g, const u32x4* __restrict__ u,
+                                                      u32x4* __restrict__ out, int64_t n8) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  const u32x4 gv = g[i], uv = u[i];
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float lo = __fmul_rn(silu_bf16(bf2f_lo(gv[j])), bf2f_lo(uv[j]));
+    const float hi = __fmul_rn(silu_bf16(bf2f_hi(gv[j])), bf2f_hi(uv[j]));
+    o[j] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  }
+  out[i] = o;
+}
+
 int launch_swiglu(hipStream_t st, const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n) {
   if (n == 0) return LISAQ_OK;
-  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n);
+  const bool vec = n % 8 == 0 && ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u) |
+                                   reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(swiglu8_kernel, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const u32x4*>(g), reinterpret_cast<const u32x4*>(u),
+                       reinterpret_cast<u32x4*>(out), n / 8);
+  else
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, out, n);
   return check_launch("swiglu");
 }
 
@@ -261,90 +289,148 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   out[i] = f2bf(total);
 }
 
+// 8 consecutive d per thread (16-byte loads of the down rows); H % 8 == 0
+__global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restrict__ down,
+                                                       const float* __restrict__ w,
+                                                       const int32_t* __restrict__ inv,
+                                                       uint16_t* __restrict__ out, int64_t T, int k,
+                                                       int64_t H) {
+  const int64_t H8 = H / 8;
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= T * H8) return;
+  const int64_t t = i / H8, d8 = i - t * H8;
+  const int TY = k < 8 ? k : 8;
+  float total[8];
+  for (int y = 0; y < TY; ++y) {
+    float acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+    for (int rr = y; rr < k; rr += TY) {
+      const float wr = w[t * k + rr];
+      const u32x4 v = reinterpret_cast<const u32x4*>(down + (int64_t)inv[t * k + rr] * H)[d8];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc[2 * c] = __fadd_rn(__fmul_rn(bf2f_lo(v[c]), wr), acc[2 * c]);
+        acc[2 * c + 1] = __fadd_rn(__fmul_rn(bf2f_hi(v[c]), wr), acc[2 * c + 1]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) total[c] = y == 0 ? acc[c] : __fadd_rn(acc[c], total[c]);
+  }
+  u32x4 o;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) o[c] = (uint32_t)f2bf(total[2 * c]) | ((uint32_t)f2bf(total[2 * c + 1]) << 16);
+  reinterpret_cast<u32x4*>(out + t * H)[d8] = o;
+}
+
 int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const int32_t* inv, uint16_t* out,
                    int64_t T, int k, int64_t H) {
   const int64_t n = T * H;
   if (n == 0) return LISAQ_OK;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, down, w, inv, out,
-                     T, k, H);
+  const bool vec = H % 8 == 0 && ((reinterpret_cast<uintptr_t>(down) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(combine8_kernel, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, st, down, w, inv,
+                       out, T, k, H);
+  else
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, down, w, inv, out,
+                       T, k, H);
   return check_launch("moe_combine");
 }
 
 // ---------------------------------------------------------------------------
-// gather_qmm tile tables.  Runs of equal consecutive expert ids are found and
-// each run becomes either matvec tiles (run length < limit: {e, start, len,
-// n tile of 32}) or matmul tiles ({e, start + i*BM, rows, n tile of BN}),
+// gather_qmm tile tables.  The sorted expert ids form one run per expert; each
+// run becomes either matvec tiles (run length < limit: {e, start, len, n tile
+// of VR rows}) or matmul tiles ({e, start + i*BM, rows, n tile of BN}),
 // matching the reference's per-run quantized_matmul dispatch.  Unused entries
 // up to each table's capacity are written as {-1,..} so a grid of `capacity`
-// workgroups can be launched without a host round trip.  One workgroup.
-__global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restrict__ ids, int64_t R,
-                                                          int N, int limit, int VR, int BM, int BN,
+// workgroups can be launched without a host round trip.  One workgroup:
+//  1. one coalesced pass marks each run's first and last index per expert
+//     (ids out of [0, E) or not sorted: no tiles at all, counts[2] = 1);
+//  2. per-expert tile counts and an exclusive scan over the experts;
+//  3. each thread writes the tiles of its experts, then the padding.
+__global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restrict__ ids, int64_t R, int E, int N,
+                                                          int limit, int VR, int BM, int BN,
                                                           int4* __restrict__ qmv_tab, int qmv_cap,
                                                           int4* __restrict__ qmm_tab, int qmm_cap,
                                                           int32_t* __restrict__ counts) {
-  __shared__ int s_qmv[1024], s_qmm[1024], s_tot[2];
+  extern __shared__ int tt_smem[];
+  int* rstart = tt_smem;      // [E] first index of expert e's run
+  int* rend = tt_smem + E;    // [E] one past its last index (0: no run)
+  __shared__ int s_q[1024], s_m[1024], s_bad;
   const int tid = threadIdx.x;
-  const int nt32 = (N + VR - 1) / VR;  // matvec tiles of VR rows
+  for (int e = tid; e < E; e += 1024) rstart[e] = rend[e] = 0;
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < R; i += 1024) {
+    const int id = ids[i];
+    const int prev = i > 0 ? ids[i - 1] : -1;
+    const int next = i + 1 < R ? ids[i + 1] : E;
+    if (id < 0 || id >= E || prev > id) {
+      s_bad = 1;  // (every writer stores the same value)
+      continue;
+    }
+    if (prev != id) rstart[id] = (int)i;
+    if (next != id) rend[id] = (int)(i + 1);
+  }
+  __syncthreads();
+  const int nt32 = (N + VR - 1) / VR;  // matvec tiles per run
   const int ntbn = (N + BN - 1) / BN;
-  // contiguous segment of the ids per thread
-  const int64_t seg = (R + 1023) / 1024;
-  const int64_t i0 = tid * seg, i1 = (i0 + seg < R) ? i0 + seg : R;
-  // entries produced by runs that START in this segment
+  const int chunk = (E + 1023) / 1024;
+  const int e0 = tid * chunk, e1 = e0 + chunk < E ? e0 + chunk : E;
   int cq = 0, cm = 0;
-  for (int64_t i = i0; i < i1; ++i) {
-    if (i > 0 && ids[i] == ids[i - 1]) continue;
-    int64_t j = i + 1;
-    while (j < R && ids[j] == ids[i]) ++j;
-    const int64_t len = j - i;
+  for (int e = e0; e < e1; ++e) {
+    const int len = rend[e] - rstart[e];
+    if (len <= 0) continue;
     if (len < limit) cq += nt32;
-    else cm += (int)((len + BM - 1) / BM) * ntbn;
+    else cm += (len + BM - 1) / BM * ntbn;
   }
-  s_qmv[tid] = cq;
-  s_qmm[tid] = cm;
+  // inclusive scan (Hillis-Steele) of the per-thread counts
+  s_q[tid] = cq;
+  s_m[tid] = cm;
   __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {
+    const int aq = tid >= d ? s_q[tid - d] : 0, am = tid >= d ? s_m[tid - d] : 0;
+    __syncthreads();
+    s_q[tid] += aq;
+    s_m[tid] += am;
+    __syncthreads();
+  }
+  const bool bad = s_bad != 0;
+  const int tot_q = bad ? 0 : s_q[1023], tot_m = bad ? 0 : s_m[1023];
   if (tid == 0) {
-    int a = 0, b = 0;
-    for (int t = 0; t < 1024; ++t) {
-      const int x = s_qmv[t], y = s_qmm[t];
-      s_qmv[t] = a;
-      s_qmm[t] = b;
-      a += x;
-      b += y;
-    }
-    counts[0] = a;
-    counts[1] = b;
-    s_tot[0] = a;
-    s_tot[1] = b;
-    counts[2] = (a > qmv_cap || b > qmm_cap) ? 1 : 0;  // overflow: ids not sorted
+    counts[0] = tot_q;
+    counts[1] = tot_m;
+    counts[2] = (bad || tot_q > qmv_cap || tot_m > qmm_cap) ? 1 : 0;
   }
-  __syncthreads();
-  int oq = s_qmv[tid], om = s_qmm[tid];
-  for (int64_t i = i0; i < i1; ++i) {
-    if (i > 0 && ids[i] == ids[i - 1]) continue;
-    int64_t j = i + 1;
-    while (j < R && ids[j] == ids[i]) ++j;
-    const int64_t len = j - i;
-    const int e = ids[i];
-    if (len < limit) {
-      for (int nt = 0; nt < nt32; ++nt, ++oq)
-        if (oq < qmv_cap) qmv_tab[oq] = make_int4(e, (int)i, (int)len, nt);
-    } else {
-      for (int64_t r0 = 0; r0 < len; r0 += BM)
-        for (int nt = 0; nt < ntbn; ++nt, ++om) {
-          const int rows = (int)((len - r0) < BM ? (len - r0) : BM);
-          if (om < qmm_cap) qmm_tab[om] = make_int4(e, (int)(i + r0), rows, nt);
-        }
+  if (!bad) {
+    int oq = s_q[tid] - cq, om = s_m[tid] - cm;
+    for (int e = e0; e < e1; ++e) {
+      const int st = rstart[e], len = rend[e] - st;
+      if (len <= 0) continue;
+      if (len < limit) {
+        for (int nt = 0; nt < nt32; ++nt, ++oq)
+          if (oq < qmv_cap) qmv_tab[oq] = make_int4(e, st, len, nt);
+      } else {
+        for (int r0 = 0; r0 < len; r0 += BM)
+          for (int nt = 0; nt < ntbn; ++nt, ++om)
+            if (om < qmm_cap) qmm_tab[om] = make_int4(e, st + r0, len - r0 < BM ? len - r0 : BM, nt);
+      }
     }
   }
-  __syncthreads();
-  const int a = s_tot[0], b = s_tot[1];
-  for (int t = a + tid; t < qmv_cap; t += 1024) qmv_tab[t] = make_int4(-1, 0, 0, 0);
-  for (int t = b + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
+  for (int t = tot_q + tid; t < qmv_cap; t += 1024) qmv_tab[t] = make_int4(-1, 0, 0, 0);
+  for (int t = tot_m + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
 }
 
-int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int N, int limit, int VR, int BM, int BN,
+int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int E, int N, int limit, int VR, int BM, int BN,
                       int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap, int32_t* counts) {
-  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), 0, st, ids, R, N, limit, VR, BM, BN, qmv_tab,
+  if (E > kTileTableMaxExperts)
+    return set_error(LISAQ_EUNSUPPORTED, "gather_qmm: E=%d experts (at most %d)", E, kTileTableMaxExperts);
+  const int lds = 2 * E * 4;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)tile_table_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return set_error(LISAQ_EHIP, "gather_tile_table: LDS %d bytes: %s", lds, hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), lds, st, ids, R, E, N, limit, VR, BM, BN, qmv_tab,
                      qmv_cap, qmm_tab, qmm_cap, counts);
   return check_launch("gather_tile_table");
 }
