@@ -64,13 +64,12 @@ LISAQ_API const char* lisaq_last_error(void);
  * qmv_batch_limit(K,N) takes the matvec path (f32 weights, per-group
  * scale*sum(x*q) + bias*sum(x), AO:405-470), larger M the matmul path
  * (weights rounded to bf16 in the tile, f32 accumulate, AO:471-489).
- * workspace: lisaq_quantized_matmul_workspace() bytes (also enough for
- * lisaq_qmv at the same M), 256-byte aligned.  Its first 128 KiB hold
- * split-K arrival counters: they must be zero before the first use, every
- * call leaves them zero, and no other entry point may write them (give
- * gather_qmm / moe_forward their own workspace).  Calls that share a
- * workspace must be ordered on one stream.  serial_rows with M rows needs
- * 128 KiB + M * (size(M=1) - 128 KiB) bytes. */
+ * workspace: lisaq_quantized_matmul_workspace() bytes, 256-byte aligned
+ * (NULL/0 when that is 0).  The matvec paths use none; the matmul path uses
+ * it for f32 split-K partials when its output grid is too small to fill the
+ * GPU (e.g. N = 5120 at M = 128) and runs unsplit, slower, when the
+ * workspace is missing or smaller.  Calls that share a workspace must be
+ * ordered on one stream. */
 LISAQ_API int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t* w, const void* scales,
                            const void* biases, void* y, int64_t M, int64_t N, int64_t K,
                            int transpose, int group_size, int bits, void* workspace,
@@ -94,6 +93,9 @@ LISAQ_API int lisaq_qmv(void* stream, const void* x, const uint32_t* w, const vo
 LISAQ_API int lisaq_qmm(void* stream, const void* x, const uint32_t* w, const void* scales,
               const void* biases, void* y, int64_t M, int64_t N, int64_t K, int group_size,
               int bits, void* workspace, size_t workspace_bytes);
+/* Workspace bytes that let lisaq_qmm split K at this shape (0: no split);
+ * the split partials of jit::affine_qmm_splitk (JM:1885-1979) are f32 here. */
+LISAQ_API size_t lisaq_qmm_workspace(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 
 /* ---- dequantize / quantize ----------------------------------------------
  * out[rows,K] (bf16) = scales*code + biases.  Replaces ops::dequantize

@@ -83,7 +83,7 @@ static int run_qmv(hipStream_t st, const QmvConfig& c, const void* x, const uint
 }
 
 static int run_qmm(hipStream_t st, const void* x, const uint32_t* w, const void* s, const void* b, void* y,
-                   int64_t M, int64_t N, int64_t K, int gs, int bits) {
+                   int64_t M, int64_t N, int64_t K, int gs, int bits, void* ws, size_t ws_bytes) {
   LISAQ_REQUIRE(K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm: K=%lld must be a multiple of 64", (long long)K);
   const QmmConfig c = qmm_config(M, N, K, gs, bits);
   QmmParams p{};
@@ -97,7 +97,8 @@ static int run_qmm(hipStream_t st, const void* x, const uint32_t* w, const void*
   p.N = (int)N;
   p.K = (int)K;
   p.G = (int)(K / gs);
-  return qmm_launch(st, c, p, bits, gs, c.grid, 1);
+  if (ws) LISAQ_REQUIRE(aligned(ws, 256), LISAQ_EINVAL_LAYOUT, "qmm: workspace must be 256-byte aligned");
+  return qmm_launch(st, c, p, bits, gs, c.grid, 1, ws, ws_bytes);
 }
 
 // Gather workspace layout: [counts 256 B][qmv table][qmm table], 256-B aligned.
@@ -170,11 +171,16 @@ int lisaq_check_layout(int64_t w_rows, int64_t w_cols, int64_t s_rows, int64_t s
   return LISAQ_OK;
 }
 
+size_t lisaq_qmm_workspace(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+  if (M <= 0 || N <= 0 || K <= 0 || gs <= 0 || K % gs || K % 64) return 0;
+  return qmm_config(M, N, K, gs, bits).ws_bytes;
+}
+
 size_t lisaq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || gs <= 0 || K % gs) return 0;
-  if (M > 32) return 0;  // matmul path: no workspace
+  if (M >= lisaq_qmv_batch_limit(K, N)) return lisaq_qmm_workspace(M, N, K, gs, bits);
   // covers both the dispatched path and the forced matvec path at this M
-  return qmv_config(M, N, K, gs, bits).ws_bytes;
+  return M <= 32 ? qmv_config(M, N, K, gs, bits).ws_bytes : 0;
 }
 
 int lisaq_qmv(void* stream, const void* x, const uint32_t* w, const void* s, const void* b, void* y,
@@ -191,14 +197,12 @@ int lisaq_qmv(void* stream, const void* x, const uint32_t* w, const void* s, con
 
 int lisaq_qmm(void* stream, const void* x, const uint32_t* w, const void* s, const void* b, void* y,
               int64_t M, int64_t N, int64_t K, int gs, int bits, void* ws, size_t ws_bytes) {
-  (void)ws;
-  (void)ws_bytes;
   g_err[0] = 0;
   int rc = validate_mm("qmm", x, w, s, b, y, M, N, K, 1, gs, bits);
   if (rc) return rc;
   if (M == 0 || N == 0) return LISAQ_OK;
   LISAQ_REQUIRE(K > 0, LISAQ_EINVAL_SHAPE, "qmm: K=0");
-  return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits);
+  return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
 }
 
 int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t* w, const void* s, const void* b,
@@ -213,7 +217,7 @@ int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t* w, const
     const QmvConfig c = qmv_config(M, N, K, gs, bits);
     return run_qmv((hipStream_t)stream, c, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
   }
-  return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits);
+  return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
 }
 
 int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32_t* w, const void* s,

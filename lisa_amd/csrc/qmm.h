@@ -12,15 +12,21 @@ struct QmmParams {
   uint16_t* y;         // [rows, N] bf16
   const int4* tiles;   // gather: {expert, row start, rows, n tile} per block, or null
   int M, N, K, G;
+  float* partial;       // split over K: [ksplit, M, N] f32 partial sums (plain launches only)
+  int ksplit;           // K splits (1: the kernel writes y)
 };
 
 struct QmmConfig {
   int MT, NT, BM, BN, grid_n, grid_m;
   int grid;  // workgroups of a plain (no tile table) launch: grid_n * grid_m
+  int S;            // K splits of a plain launch (1: none)
+  size_t ws_bytes;  // workspace for the split partials (0 when S == 1)
 };
 
 QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+// Enqueue.  A plain launch whose config splits K uses ws (>= c.ws_bytes) for
+// the partials, or runs unsplit when ws is missing or too small.
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
-               int grid_y);
+               int grid_y, void* ws = nullptr, size_t ws_bytes = 0);
 
 }  // namespace lisaq

@@ -120,7 +120,7 @@ struct QmmLds {
   static constexpr int TOTAL = NBUF * (X + WSTAGE);
 };
 
-template <int BITS, int GS, int MT, int NT>
+template <int BITS, int GS, int MT, int NT, bool SPLIT>
 __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
   using L = QmmLds<BITS, GS, MT, NT>;
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   const uint16_t* x = p.x;
   uint16_t* y = p.y;
   int M = p.M;
-  int m0, nt0;
+  int m0, nt0, split = 0;
   if (p.tiles) {
     const int4 t = p.tiles[blockIdx.x];
     if (t.x < 0) return;
@@ -153,10 +153,13 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     m0 = 0;
     nt0 = t.w * BN;
   } else {
-    // row-block major: consecutive workgroups share an x row block and walk W
-    const int gn = (p.N + BN - 1) / BN;
-    nt0 = (blockIdx.x % gn) * BN;
-    m0 = (blockIdx.x / gn) * BM;
+    // row-block major: consecutive workgroups share an x row block and walk W;
+    // with a split over K, split s of every tile comes after split s-1's
+    const int gn = (p.N + BN - 1) / BN, T = gn * ((M + BM - 1) / BM);
+    const int tile = blockIdx.x % T;
+    split = blockIdx.x / T;
+    nt0 = (tile % gn) * BN;
+    m0 = (tile / gn) * BM;
   }
 
   // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
@@ -164,14 +167,14 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   // x: BM/8 instructions of 1 KB, XI per wave; lane l fills row 8g + l/8,
   // physical chunk l%8 (= logical chunk (l%8) ^ (row%8))
   constexpr int XI = BM / 8 / 4;
-  uint32_t xoff[XI];  // element offsets (the host checks x fits 2^31 elements)
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int r = (wave * XI + i) * 8 + (lane >> 3);
-    int row = m0 + r;
-    row = row < M ? row : M - 1;
-    xoff[i] = (uint32_t)row * (uint32_t)p.K + (uint32_t)(((lane & 7) ^ (r & 7)) << 3);
-  }
+  // element offsets, recomputed per copy to save registers (the host checks
+  // that x fits 2^31 elements); the chunk swizzle uses row % 8 = lane / 8
+  const int xrow0 = m0 + wave * XI * 8 + (lane >> 3);
+  const uint32_t xchunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 3);
+  auto xoff = [&](int i) -> uint32_t {
+    const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
+    return (uint32_t)row * (uint32_t)p.K + xchunk;
+  };
   // W: BN rows x RB bytes, row-major; 16 bytes per lane, WI instructions per wave
   constexpr int WLPR = L::RB / 16;             // lanes per row
   constexpr int WI = L::W / 1024 / 4;          // instructions per wave
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     unsigned char* st = smem + stage * L::X;
     const int k0 = k * BK;
 #pragma unroll
-    for (int i = 0; i < XI; ++i) load_lds16(x + xoff[i] + k0, st + (wave * XI + i) * XG);
+    for (int i = 0; i < XI; ++i) load_lds16(x + xoff(i) + k0, st + (wave * XI + i) * XG);
   };
   auto issue_w = [&](int k, int stage) {
     unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
@@ -260,11 +263,15 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   // earlier); meanwhile the copies of x(k+2) and W(k+3) are in flight.  Copies
   // past the last step re-read it, so every step issues the same number of
   // copies and the waits are constants.
-  const int nk = p.K / BK;
-  auto kc = [&](int k) { return k < nk ? k : nk - 1; };
+  // K-steps of this workgroup: [kb, kb + nk) (the whole K unless split)
+  const int nk_all = p.K / BK;
+  const int per = (nk_all + p.ksplit - 1) / p.ksplit;
+  const int kb = split * per;
+  const int nk = nk_all - kb < per ? nk_all - kb : per;  // (host: every split has >= 1 step)
+  auto kc = [&](int k) { return kb + (k < nk ? k : nk - 1); };
   uint32_t bop[NT][16];
-  issue_x(0, 0);
-  issue_w(0, 0);
+  issue_x(kc(0), 0);
+  issue_w(kc(0), 0);
   issue_w(kc(1), 1);
   issue_x(kc(1), 1);
   issue_w(kc(2), 2);
@@ -272,7 +279,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   __syncthreads();
   {
     WLane w0;
-    read_w(0, 0, w0);
+    read_w(kc(0), 0, w0);
 #pragma unroll
     for (int jw = 0; jw < G::WPL; ++jw) dequant_word(w0, jw, bop);
   }
@@ -308,19 +315,39 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     ws1 = ws1 == 2 ? 0 : ws1 + 1;
   }
 
-  // epilogue: D[m][n], lane holds n = col, rows 8*(i/4) + 4*h + (i%4)
+  // epilogue: D[m][n], lane holds n = col, rows 8*(i/4) + 4*h + (i%4); a
+  // split writes its f32 partial instead (one uniform branch around the
+  // whole store loop keeps the accumulators in registers)
+  auto store = [&](auto put) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int n = nt0 + (wave * NT + nt) * 32 + col;
-    if (n >= p.N) continue;
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = nt0 + (wave * NT + nt) * 32 + col;
+      if (n >= p.N) continue;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-        if (m < M) y[(int64_t)m * p.N + n] = f2bf(acc[mt][nt][i]);
-      }
+        for (int i = 0; i < 16; ++i) {
+          const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (m < M) put(m, n, acc[mt][nt][i]);
+        }
+    }
+  };
+  if constexpr (SPLIT) {
+    float* part = p.partial + (int64_t)split * M * p.N;
+    store([&](int m, int n, float v) { part[(int64_t)m * p.N + n] = v; });
+  } else {
+    store([&](int m, int n, float v) { y[(int64_t)m * p.N + n] = f2bf(v); });
   }
+}
+
+// y = bf16(sum over the splits of the f32 partials), splits added in order.
+__global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __restrict__ part,
+                                                               uint16_t* __restrict__ y, int64_t MN, int S) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= MN) return;
+  float v = part[i];
+  for (int s = 1; s < S; ++s) v += part[(int64_t)s * MN + i];
+  y[i] = f2bf(v);
 }
 
 // ---------------------------------------------------------------------------
@@ -337,6 +364,22 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   c.grid_n = (int)((N + c.BN - 1) / c.BN);
   c.grid_m = (int)((M + c.BM - 1) / c.BM);
   c.grid = c.grid_n * c.grid_m;  // 1-D launch (see the kernel's tile order)
+  // Far too few tiles for the 256 CUs (e.g. N = 5120 at M = 128: 20 tiles):
+  // split K, up to about two workgroups per CU, each split at least 8
+  // K-steps.  (Measured: at 136-160 tiles a split of 2 is already slower.)
+  c.S = 1;
+  const int nk = (int)(K / 64);
+  if (c.grid < 128)
+    while (c.grid * c.S * 2 <= 512 && nk / (c.S * 2) >= 8) c.S *= 2;
+  if (const char* env = getenv("LISAQ_QMM_SPLIT")) {
+    const int v = atoi(env);
+    if (v >= 1 && v <= nk) c.S = v;
+  }
+  if (c.S > 1) {
+    const int per = (nk + c.S - 1) / c.S;
+    c.S = (nk + per - 1) / per;  // every split non-empty
+  }
+  c.ws_bytes = c.S > 1 ? (size_t)c.S * M * N * 4 : 0;
   (void)K;
   (void)gs;
   (void)bits;
@@ -355,20 +398,23 @@ static int qmm_lds_bytes(int MT, int bits, int gs) {
   return gs == 32 ? pick(QmmLds<2, 32, 4, 2>{}) : pick(QmmLds<2, 64, 4, 2>{});
 }
 
-template <int MT>
+template <int MT, bool SPLIT>
 static qmm_fn qmm_kernel_for(int bits, int gs) {
-  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, MT, 2>;
-  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, MT, 2>;
-  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, MT, 2>;
-  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, MT, 2>;
-  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, MT, 2>;
-  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, MT, 2>;
+  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, MT, 2, SPLIT>;
+  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, MT, 2, SPLIT>;
+  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, MT, 2, SPLIT>;
+  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, MT, 2, SPLIT>;
+  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, MT, 2, SPLIT>;
+  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, MT, 2, SPLIT>;
   return nullptr;
 }
 
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
-               int grid_y) {
-  qmm_fn fn = c.MT == 8 ? qmm_kernel_for<8>(bits, gs) : qmm_kernel_for<4>(bits, gs);
+               int grid_y, void* ws, size_t ws_bytes) {
+  // split over K only for plain launches with room for the partials
+  const bool split = !p.tiles && c.S > 1 && ws != nullptr && ws_bytes >= c.ws_bytes;
+  qmm_fn fn = c.MT == 8 ? (split ? qmm_kernel_for<8, true>(bits, gs) : qmm_kernel_for<8, false>(bits, gs))
+                        : (split ? qmm_kernel_for<4, true>(bits, gs) : qmm_kernel_for<4, false>(bits, gs));
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);
   const int lds = qmm_lds_bytes(c.MT, bits, gs);
   if (lds > 64 * 1024) {
@@ -376,8 +422,15 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
     if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmm: LDS %d bytes: %s", lds, hipGetErrorString(e));
   }
   LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
-  hipLaunchKernelGGL(fn, dim3(grid_x, grid_y), dim3(256), lds, stream, p);
-  return check_launch("qmm");
+  p.ksplit = split ? c.S : 1;
+  p.partial = split ? static_cast<float*>(ws) : nullptr;
+  hipLaunchKernelGGL(fn, dim3(split ? grid_x * c.S : grid_x, grid_y), dim3(256), lds, stream, p);
+  int rc = check_launch("qmm");
+  if (rc || !split) return rc;
+  const int64_t MN = (int64_t)p.M * p.N;
+  hipLaunchKernelGGL(qmm_split_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, stream,
+                     (const float*)p.partial, p.y, MN, c.S);
+  return check_launch("qmm_split_reduce");
 }
 
 }  // namespace lisaq

@@ -35,10 +35,9 @@ _ws: dict = {}
 def workspace(device: torch.device, nbytes: int, kind: str = "linear") -> torch.Tensor:
     """A zero-initialised scratch buffer of at least ``nbytes`` on ``device``.
 
-    ``kind`` "linear" is the quantized-matmul workspace, whose split-K arrival
-    counters the library leaves at zero after every call, so it is reused by
-    calls ordered on one stream; "moe" is scratch for gather_qmm / moe_forward,
-    kept apart so their tile tables never land on those counters."""
+    ``kind`` "linear" is the quantized-matmul workspace (split-K partials of
+    the matmul path), reused by calls ordered on one stream; "moe" is scratch
+    for gather_qmm / moe_forward (tile tables, intermediates)."""
     key = (device.type, device.index, kind)
     nbytes = max(int(nbytes), 256)
     with _ws_lock:
@@ -106,7 +105,7 @@ def _mm(entry: str, x, w, scales, biases, transpose, group_size, bits):
     y = torch.empty(*x.shape[:-1], N, dtype=torch.bfloat16, device=x.device)
     lib = _lib.load()
     if entry == "lisaq_qmm":
-        nbytes = 0
+        nbytes = lib.lisaq_qmm_workspace(M, N, K, group_size, bits)
     elif entry == "lisaq_quantized_matmul_serial_rows":
         nbytes = lib.lisaq_quantized_matmul_workspace(1, N, K, group_size, bits)
         nbytes = nbytes and nbytes + (M - 1) * (nbytes - QMV_COUNTER_BYTES)

@@ -97,6 +97,21 @@ def test_qmm_parity(dev, oracle, M, N, K, bits, gs):
         assert np.array_equal(got, got2)
 
 
+@pytest.mark.parametrize("split", ["1", "2", "3", "7"])
+def test_qmm_split_k(dev, oracle, monkeypatch, split):
+    """The matmul split over K (f32 partials in the workspace, summed in split
+    order): every split count against the oracle, and the same bits on a repeat."""
+    monkeypatch.setenv("LISAQ_QMM_SPLIT", split)
+    rng = np.random.default_rng(77)
+    M, N, K = 70, 300, 1024
+    w, s, b = np_linear(rng, N, K, 4, 64)
+    x = np_x(rng, M, K)
+    ref = oracle.qmm(x, w, s, b, 64, 4)
+    got = _run(ops.qmm, dev, x, w, s, b, 64, 4)
+    assert_close_bf16(got, ref, what=f"qmm split={split}")
+    assert np.array_equal(_run(ops.qmm, dev, x, w, s, b, 64, 4), got)
+
+
 @pytest.mark.parametrize("M,N,K,bits", [(128, 17408, 5120, 4), (512, 5120, 17408, 4), (2048, 17408, 5120, 4),
                                         (512, 17408, 5120, 2)])
 def test_qmm_prefill_shapes_sampled_rows(dev, oracle, M, N, K, bits):
