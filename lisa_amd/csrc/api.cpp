@@ -111,20 +111,74 @@ struct GatherLayout {
 
 static size_t up256(size_t v) { return (v + 255) / 256 * 256; }
 
-static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs, int bits) {
+// max_run: an upper bound of the longest run of equal ids when the caller
+// knows one (moe_forward: a token picks an expert at most once, so T);
+// otherwise R.  It only sizes the matvec rows and decides if matmul tiles can
+// occur; the tables still follow the actual runs.
+static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs, int bits, int64_t max_run = 0) {
   GatherLayout L{};
   L.limit = lisaq_qmv_batch_limit(K, N);
   const int64_t runs = R < E ? R : E;
-  L.Mmax = (int)((R < L.limit - 1) ? R : L.limit - 1);
+  const int64_t mr = (max_run > 0 && max_run < R) ? max_run : R;
+  L.Mmax = (int)((mr < L.limit - 1) ? mr : L.limit - 1);
   if (L.Mmax < 1) L.Mmax = 1;
   L.qc = qmv_config(L.Mmax, N, K, gs, bits, /*single_pass=*/true);
   L.mc = qmm_config(L.limit, N, K, gs, bits);
   L.qmv_cap = (int)(runs * ((N + L.qc.tile_rows - 1) / L.qc.tile_rows));
-  L.qmm_cap = (R >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
+  L.qmm_cap = (mr >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
   L.qmv_off = 256;
   L.qmm_off = L.qmv_off + up256((size_t)L.qmv_cap * 16);
   L.total = L.qmm_off + up256((size_t)L.qmm_cap * 16);
   return L;
+}
+
+// Tile tables of a gather (runs of the sorted ids) into the workspace.
+static int gather_tables(hipStream_t st, const GatherLayout& L, const int32_t* rhs, int64_t R, int64_t N, int E,
+                         void* ws) {
+  char* base = (char*)ws;
+  return launch_tile_table(st, rhs, R, E, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN,
+                           (int4*)(base + L.qmv_off), L.qmv_cap, (int4*)(base + L.qmm_off), L.qmm_cap,
+                           (int32_t*)base);
+}
+
+// The matvec and matmul launches over built tables (several weight stacks of
+// the same shape may share one set of tables).
+static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, const uint32_t* w, const void* s,
+                         const void* b, void* y, int64_t R, int64_t N, int64_t K, int gs, int bits, void* ws) {
+  char* base = (char*)ws;
+  int rc;
+  if (L.qmv_cap > 0) {
+    QmvParams p{};
+    p.x = (const uint16_t*)x;
+    p.w = w;
+    p.s = (const uint16_t*)s;
+    p.b = (const uint16_t*)b;
+    p.y = (uint16_t*)y;
+    p.tiles = (const int4*)(base + L.qmv_off);
+    p.M = L.Mmax;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.G = (int)(K / gs);
+    p.part_rows = (int)R;
+    rc = qmv_launch(st, L.qc, p, bits, gs, L.qmv_cap);
+    if (rc) return rc;
+  }
+  if (L.qmm_cap > 0) {
+    QmmParams p{};
+    p.x = (const uint16_t*)x;
+    p.w = w;
+    p.s = (const uint16_t*)s;
+    p.b = (const uint16_t*)b;
+    p.y = (uint16_t*)y;
+    p.tiles = (const int4*)(base + L.qmm_off);
+    p.M = (int)R;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.G = (int)(K / gs);
+    rc = qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
+    if (rc) return rc;
+  }
+  return LISAQ_OK;
 }
 
 }  // namespace lisaq
@@ -347,45 +401,9 @@ int lisaq_gather_qmm(void* stream, const void* x, const uint32_t* w, const void*
   if (L.qmm_cap > 0)
     LISAQ_REQUIRE(K % 64 == 0, LISAQ_EUNSUPPORTED, "gather_qmm: K=%lld must be a multiple of 64", (long long)K);
   hipStream_t st = (hipStream_t)stream;
-  char* base = (char*)ws;
-  int32_t* counts = (int32_t*)base;
-  int4* qmv_tab = (int4*)(base + L.qmv_off);
-  int4* qmm_tab = (int4*)(base + L.qmm_off);
-  rc = launch_tile_table(st, rhs, R, E, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN, qmv_tab, L.qmv_cap, qmm_tab,
-                         L.qmm_cap, counts);
+  rc = gather_tables(st, L, rhs, R, N, E, ws);
   if (rc) return rc;
-  if (L.qmv_cap > 0) {
-    QmvParams p{};
-    p.x = (const uint16_t*)x;
-    p.w = w;
-    p.s = (const uint16_t*)s;
-    p.b = (const uint16_t*)b;
-    p.y = (uint16_t*)y;
-    p.tiles = qmv_tab;
-    p.M = L.Mmax;
-    p.N = (int)N;
-    p.K = (int)K;
-    p.G = (int)(K / gs);
-    p.part_rows = (int)R;
-    rc = qmv_launch(st, L.qc, p, bits, gs, L.qmv_cap);
-    if (rc) return rc;
-  }
-  if (L.qmm_cap > 0) {
-    QmmParams p{};
-    p.x = (const uint16_t*)x;
-    p.w = w;
-    p.s = (const uint16_t*)s;
-    p.b = (const uint16_t*)b;
-    p.y = (uint16_t*)y;
-    p.tiles = qmm_tab;
-    p.M = (int)R;
-    p.N = (int)N;
-    p.K = (int)K;
-    p.G = (int)(K / gs);
-    rc = qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
-    if (rc) return rc;
-  }
-  return LISAQ_OK;
+  return gather_launch(st, L, x, w, s, b, y, R, N, K, gs, bits, ws);
 }
 
 int lisaq_swiglu(void* stream, const void* gate, const void* up, void* act, int64_t n) {
@@ -475,10 +493,21 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   if ((rc = lisaq_moe_route(st, logits, T, E, k, idx, wts))) return rc;
   if ((rc = lisaq_moe_sort(st, idx, R, E, k, sorted, order, rows, inv, offs))) return rc;
   if ((rc = lisaq_gather_rows(st, x, rows, xs, R, H))) return rc;
-  if ((rc = lisaq_gather_qmm(st, xs, gw, gsc, gbi, sorted, g, R, I, H, E, 1, gs, bits, gws, gws_bytes))) return rc;
-  if ((rc = lisaq_gather_qmm(st, xs, uw, usc, ubi, sorted, u, R, I, H, E, 1, gs, bits, gws, gws_bytes))) return rc;
+  // gate and up share one set of tile tables; every run is at most T rows
+  if ((rc = validate_mm("moe_forward gate", xs, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
+  if ((rc = validate_mm("moe_forward up", xs, uw, usc, ubi, u, R, I, H, 1, gs, bits))) return rc;
+  if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, d, R, H, I, 1, gs, bits))) return rc;
+  const GatherLayout GU = gather_layout(R, I, H, E, gs, bits, T);
+  const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T);
+  LISAQ_REQUIRE(GU.total <= gws_bytes && DN.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
+  if ((GU.qmm_cap > 0 || DN.qmm_cap > 0) && (H % 64 || I % 64))
+    return set_error(LISAQ_EUNSUPPORTED, "moe_forward: H, I must be multiples of 64 for the matmul path");
+  if ((rc = gather_tables(st, GU, sorted, R, I, E, gws))) return rc;
+  if ((rc = gather_launch(st, GU, xs, gw, gsc, gbi, g, R, I, H, gs, bits, gws))) return rc;
+  if ((rc = gather_launch(st, GU, xs, uw, usc, ubi, u, R, I, H, gs, bits, gws))) return rc;
   if ((rc = lisaq_swiglu(st, g, u, g, R * I))) return rc;
-  if ((rc = lisaq_gather_qmm(st, g, dw, dsc, dbi, sorted, d, R, H, I, E, 1, gs, bits, gws, gws_bytes))) return rc;
+  if ((rc = gather_tables(st, DN, sorted, R, H, E, gws))) return rc;
+  if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;
   return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
 }
 

@@ -356,7 +356,7 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   extern __shared__ int tt_smem[];
   int* rstart = tt_smem;      // [E] first index of expert e's run
   int* rend = tt_smem + E;    // [E] one past its last index (0: no run)
-  __shared__ int s_q[1024], s_m[1024], s_bad;
+  __shared__ int s_q[16], s_m[16], s_bad;
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += 1024) rstart[e] = rend[e] = 0;
   if (tid == 0) s_bad = 0;
@@ -384,26 +384,42 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
     if (len < limit) cq += nt32;
     else cm += (len + BM - 1) / BM * ntbn;
   }
-  // inclusive scan (Hillis-Steele) of the per-thread counts
-  s_q[tid] = cq;
-  s_m[tid] = cm;
+  // inclusive scan of the per-thread counts: within each wave by shuffles,
+  // then the 16 wave totals
+  const int lane = tid & 63, wv = tid >> 6;
+  int iq = cq, im = cm;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int aq = __shfl_up(iq, d), am = __shfl_up(im, d);
+    if (lane >= d) {
+      iq += aq;
+      im += am;
+    }
+  }
+  if (lane == 63) {
+    s_q[wv] = iq;
+    s_m[wv] = im;
+  }
   __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {
-    const int aq = tid >= d ? s_q[tid - d] : 0, am = tid >= d ? s_m[tid - d] : 0;
-    __syncthreads();
-    s_q[tid] += aq;
-    s_m[tid] += am;
-    __syncthreads();
+  int bq = 0, bm = 0;
+  for (int w2 = 0; w2 < wv; ++w2) {
+    bq += s_q[w2];
+    bm += s_m[w2];
+  }
+  int tq = 0, tm = 0;
+  for (int w2 = 0; w2 < 16; ++w2) {
+    tq += s_q[w2];
+    tm += s_m[w2];
   }
   const bool bad = s_bad != 0;
-  const int tot_q = bad ? 0 : s_q[1023], tot_m = bad ? 0 : s_m[1023];
+  const int tot_q = bad ? 0 : tq, tot_m = bad ? 0 : tm;
   if (tid == 0) {
     counts[0] = tot_q;
     counts[1] = tot_m;
     counts[2] = (bad || tot_q > qmv_cap || tot_m > qmm_cap) ? 1 : 0;
   }
   if (!bad) {
-    int oq = s_q[tid] - cq, om = s_m[tid] - cm;
+    int oq = bq + iq - cq, om = bm + im - cm;
     for (int e = e0; e < e1; ++e) {
       const int st = rstart[e], len = rend[e] - st;
       if (len <= 0) continue;

@@ -103,6 +103,22 @@ def test_gather_qmm_parity(dev, oracle, R, E, N, K):
     assert_close_bf16(from_dev_bf16(y), ref, what=f"gather R={R} E={E} N={N} K={K}")
 
 
+@pytest.mark.parametrize("kernel", ["d", "t"])
+@pytest.mark.parametrize("R,E,N,K", [(1, 4, 768, 2048), (2, 4, 768, 2048), (2, 2, 2048, 768), (2, 1, 300, 512)])
+def test_gather_qmm_short_runs(dev, oracle, monkeypatch, kernel, R, E, N, K):
+    """Runs of one or two rows (decode MoE) through each tile-capable matvec
+    kernel (forced with LISAQ_QMV_KERNEL)."""
+    monkeypatch.setenv("LISAQ_QMV_KERNEL", kernel)
+    rng = np.random.default_rng(R * 11 + E + N)
+    W, S, B = _expert_stack(rng, E, N, K)
+    ids = np.sort(rng.integers(0, E, R)).astype(np.int32)
+    x = np_x(rng, R, K)
+    y = ops.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(W, dev), to_dev_bf16(S, dev), to_dev_bf16(B, dev),
+                       rhs_indices=to_dev(ids, dev), group_size=64, bits=4)
+    ref = _gather_ref(oracle, x, W, S, B, ids, ops.qmv_batch_limit(K, N))
+    assert_close_bf16(from_dev_bf16(y), ref, what=f"gather[{kernel}] R={R} E={E} N={N} K={K}")
+
+
 @pytest.mark.parametrize("T", [1, 4, 64])
 def test_moe_forward_parity(dev, oracle, T):
     """Whole routed SwitchGLU vs the oracle chain, with the reference shapes
@@ -140,7 +156,10 @@ def test_moe_forward_parity(dev, oracle, T):
     dref = _gather_ref(oracle, from_dev_bf16(act), *D, srt, ops.qmv_batch_limit(I, H))
     assert_close_bf16(from_dev_bf16(dd), dref, what="down")
     comb = ops.moe_combine(dd, wts.reshape(-1), to_dev(inv, dev), T, k)
-    # the fused entry point runs the same kernels in the same order: identical bits
-    assert np.array_equal(from_dev_bf16(out), from_dev_bf16(comb))
+    # the fused entry point may pick other matvec kernels (it knows that a run
+    # is at most T rows): same result within the output tolerance
+    from lisa_amd.synth import bf16_bits_to_f32
+
+    assert_close_bf16(from_dev_bf16(out), bf16_bits_to_f32(from_dev_bf16(comb)), what="moe_forward vs step by step")
     assert np.array_equal(from_dev_bf16(comb), oracle.moe_combine(from_dev_bf16(dd), wts.cpu().numpy(), inv, T, k))
     torch.cuda.synchronize()
