@@ -54,6 +54,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-qmm", action="store_true")
+    ap.add_argument("--no-table", action="store_true", help="skip the per-configuration table")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run a plain 64 MiB device copy (the reference kernel for the HBM byte counters)")
     args = ap.parse_args()
@@ -146,6 +147,9 @@ def main():
     flops = 2.0 * Mq * N * K
     tflops = flops / qmm_s / 1e12
 
+    # --- the other measured configurations (parity cases of the same path) ----
+    table = [] if args.no_table else config_table(dev, gen, stream)
+
     # --- CPU baseline (oracle fused dequant-dot, same shape, bounded sample) ---
     cpu = None
     if not args.no_cpu:
@@ -184,8 +188,104 @@ def main():
                          "traffic": QMM_TRAFFIC_BYTES, "kernel": QMM_KERNEL},
         },
         "cpu_baseline": cpu,
+        "configs": table,
     }
     print(json.dumps(out), flush=True)
+
+
+def _time_graph(stream, fn, n_sets, steps):
+    """Average seconds per call of fn(i) over `steps` calls replayed from a HIP graph (i cycles
+    over n_sets inputs), after one warm-up pass."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        for i in range(n_sets):
+            fn(i)
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(steps):
+            fn(i)
+    with torch.cuda.stream(stream):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def config_table(dev, gen, stream):
+    """Every measured configuration of the path (BASELINE configs [1]-[4]), cold weights:
+    distinct weight sets in rotation so more than the 256 MB Infinity Cache is streamed."""
+    import torch
+
+    from lisa_amd import ops
+    from lisa_amd.synth import torch_linear, torch_x
+
+    rows = []
+    gs = 64
+
+    def qmv_row(name, M, N, K, bits, n_sets, steps=200):
+        sets = [torch_linear(N, K, bits, gs, device=dev, generator=gen) for _ in range(n_sets)]
+        x = torch_x(M, K, device=dev, generator=gen)
+        t = _time_graph(stream, lambda i: ops.quantized_matmul(x, *sets[i % n_sets], True, gs, bits), n_sets, steps)
+        nb = qmv_bytes(M, N, K, bits, gs)
+        rows.append({"workload": name, "M": M, "N": N, "K": K, "bits": bits, "us": round(t * 1e6, 2),
+                     "value": round(nb / t / 1e9, 1), "unit": "GB/s", "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4),
+                     "bytes_per_call": nb, "weight_sets": n_sets})
+        del sets
+
+    def qmm_row(name, M, N, K, bits, steps=10):
+        w = torch_linear(N, K, bits, gs, device=dev, generator=gen)
+        x = torch_x(M, K, device=dev, generator=gen)
+        t = _time_graph(stream, lambda i: ops.quantized_matmul(x, *w, True, gs, bits), 1, steps)
+        fl = 2.0 * M * N * K
+        rows.append({"workload": name, "M": M, "N": N, "K": K, "bits": bits, "us": round(t * 1e6, 1),
+                     "value": round(fl / t / 1e12, 1), "unit": "TFLOP/s",
+                     "frac": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4)})
+
+    # [1] decode: up 9728x2560 and down 2560x9728 (14 MB each; 20 sets), M = 1, 2, 4, 8
+    for M in (1, 2, 4, 8):
+        qmv_row("decode up 4-bit", M, 9728, 2560, 4, 20)
+        qmv_row("decode down 4-bit", M, 2560, 9728, 4, 20)
+    # north-star shape at M = 2, 4, 8 (8 sets)
+    for M in (2, 4, 8):
+        qmv_row("north-star shape 4-bit", M, 17408, 5120, 4, 8)
+    # [3] 2-bit decode
+    qmv_row("decode 2-bit", 1, 17408, 5120, 2, 10)
+    # [2] prefill: up 17408x5120 and down 5120x17408, M = 128, 512, 2048; [3] 2-bit M = 512
+    for M in (128, 512, 2048):
+        qmm_row("prefill up 4-bit", M, 17408, 5120, 4)
+        qmm_row("prefill down 4-bit", M, 5120, 17408, 4)
+    qmm_row("prefill up 2-bit", 512, 17408, 5120, 2)
+    # [4] MoE: E=128, k=8, H=2048, I=768 (gate/up/down stacks, 340 MB); T=1 with rotating logits
+    # (different experts each call), T=4096
+    E, k, H, I = 128, 8, 2048, 768
+    gate = torch_linear(I, H, 4, gs, device=dev, generator=gen, experts=E)
+    up = torch_linear(I, H, 4, gs, device=dev, generator=gen, experts=E)
+    down = torch_linear(H, I, 4, gs, device=dev, generator=gen, experts=E)
+    for T, n_logits, steps in ((1, 32, 100), (4096, 1, 5)):
+        x = torch_x(T, H, device=dev, generator=gen)
+        logits = [torch.randn(T, E, device=dev, generator=gen) for _ in range(n_logits)]
+        t = _time_graph(stream, lambda i: ops.moe_forward(x, logits[i % n_logits], gate, up, down, k), n_logits, steps)
+        per_expert = 3 * (I * H // 2 + 2 * 2 * I * (H // gs))  # packed W + scales + biases of one expert's 3 matrices
+        if T == 1:
+            nb = k * per_expert
+            rows.append({"workload": "MoE 4-bit E=128 k=8 (route+sort+gather+gate/up/down+combine)", "T": T,
+                         "us": round(t * 1e6, 2), "value": round(nb / t / 1e9, 1), "unit": "GB/s",
+                         "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nb})
+        else:
+            fl = 2.0 * T * k * (2 * I * H + H * I)
+            rows.append({"workload": "MoE 4-bit E=128 k=8 (route+sort+gather+gate/up/down+combine)", "T": T,
+                         "us": round(t * 1e6, 1), "value": round(fl / t / 1e12, 1), "unit": "TFLOP/s",
+                         "frac": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4)})
+    return rows
 
 
 def cpu_baseline(M, N, K, bits, gs, seconds):

@@ -108,9 +108,9 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
-template <int BITS, int GS, int MT, int NT>
+template <int BITS, int GS, int MT, int NT, int WM>
 struct QmmLds {
-  static constexpr int BM = 32 * MT, BN = 4 * 32 * NT;
+  static constexpr int BM = 32 * MT * WM, BN = 4 * 32 * NT;
   static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
   static constexpr int X = BM / 8 * XG;            // x tile
   static constexpr int W = BN * RB;                // packed W tile
@@ -120,16 +120,20 @@ struct QmmLds {
   static constexpr int TOTAL = NBUF * (X + WSTAGE);
 };
 
-template <int BITS, int GS, int MT, int NT, bool SPLIT>
-__global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
+// WM waves along M (1: four waves, each BM rows x 32*NT columns, one wave
+// per SIMD; 2: eight waves, two per SIMD, each half of the rows).
+template <int BITS, int GS, int MT, int NT, int WM, bool SPLIT>
+__global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
-  using L = QmmLds<BITS, GS, MT, NT>;
+  using L = QmmLds<BITS, GS, MT, NT, WM>;
   constexpr int BM = L::BM;
   constexpr int BN = L::BN;
+  constexpr int NWV = 4 * WM;  // waves per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int wn = wave & 3, wm = wave >> 2;  // column group, row half
   const int col = lane & 31;
   const int h = lane >> 5;
 
@@ -166,7 +170,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   // matrix are clamped to the last one, their results are never stored)
   // x: BM/8 instructions of 1 KB, XI per wave; lane l fills row 8g + l/8,
   // physical chunk l%8 (= logical chunk (l%8) ^ (row%8))
-  constexpr int XI = BM / 8 / 4;
+  constexpr int XI = BM / 8 / NWV;
   // element offsets, recomputed per copy to save registers (the host checks
   // that x fits 2^31 elements); the chunk swizzle uses row % 8 = lane / 8
   const int xrow0 = m0 + wave * XI * 8 + (lane >> 3);
@@ -175,26 +179,27 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
     return (uint32_t)row * (uint32_t)p.K + xchunk;
   };
-  // W: BN rows x RB bytes, row-major; 16 bytes per lane, WI instructions per wave
-  constexpr int WLPR = L::RB / 16;             // lanes per row
-  constexpr int WI = L::W / 1024 / 4;          // instructions per wave
-  static_assert(WI >= 1 && L::W % 4096 == 0, "W tile geometry");
+  // W: BN rows x RB bytes, row-major; 16 bytes per lane: WB bytes per wave in
+  // WI instructions (the last lanes idle when a wave's share is under 1 KB)
+  constexpr int WB = L::W / NWV;                  // bytes per wave
+  constexpr int WI = WB >= 1024 ? WB / 1024 : 1;  // instructions per wave
+  constexpr int WLANES = WB >= 1024 ? 64 : WB / 16;
+  static_assert(L::W % NWV == 0 && (WB >= 1024 ? WB % 1024 == 0 : WB % 16 == 0), "W tile geometry");
   const unsigned char* wsrc[WI];
   const int64_t rowbytes = (int64_t)p.K * BITS / 8;
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
-    const int r = (wave * WI + i) * (64 / WLPR) + lane / WLPR;
-    int n = nt0 + r;
+    const int off = wave * WB + i * 1024 + lane * 16;  // byte in the W tile
+    int n = nt0 + off / L::RB;
     n = n < p.N ? n : p.N - 1;
-    wsrc[i] = reinterpret_cast<const unsigned char*>(w) + n * rowbytes + (lane % WLPR) * 16;
+    wsrc[i] = reinterpret_cast<const unsigned char*>(w) + n * rowbytes + off % L::RB;
   }
   // scales / biases: per row the 4-byte-aligned bf16 pair holding the step's
   // group(s); 64 rows per instruction (BN/64 instructions per array, spread
   // over the waves)
   constexpr int SI = BN / 64;                  // instructions per array
-  static_assert(SI % 4 == 0 || SI == 2, "scale tile geometry");
-
-  constexpr int SBI = (SI * 2 + 3) / 4;         // scale/bias instructions per wave
+  constexpr int SBI = SI * 2 / NWV;            // scale/bias instructions per wave
+  static_assert(SBI >= 1 && SI * 2 % NWV == 0, "scale tile geometry");
   constexpr int VM_X = XI, VM_W = WI + SBI;    // DMA instructions per wave: x tile, W stage
   auto issue_x = [&](int k, int stage) {
     unsigned char* st = smem + stage * L::X;
@@ -206,12 +211,13 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
     const int k0 = k * BK;
 #pragma unroll
-    for (int i = 0; i < WI; ++i) load_lds16(wsrc[i] + (int64_t)k0 * BITS / 8, st + (wave * WI + i) * 1024);
-    // 2*SI scale/bias instructions over the 4 waves
+    for (int i = 0; i < WI; ++i)
+      if (WLANES == 64 || lane < WLANES) load_lds16(wsrc[i] + (int64_t)k0 * BITS / 8, st + wave * WB + i * 1024);
+    // 2*SI scale/bias instructions over the waves
     const int g = k0 / GS;
 #pragma unroll
     for (int i = 0; i < SBI; ++i) {
-      const int idx = wave + 4 * i;  // 0 .. 2*SI-1: s row blocks, then b row blocks
+      const int idx = wave + NWV * i;  // 0 .. 2*SI-1: s row blocks, then b row blocks
       const bool is_b = idx >= SI;
       const int blk = is_b ? idx - SI : idx;
       // (lanes of this instruction load rows blk*64 + lane)
@@ -232,7 +238,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
     const int g0 = k * BK / GS;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int r = (wave * NT + nt) * 32 + col;
+      const int r = (wn * NT + nt) * 32 + col;
       // half of the staged pair: the lane's group (gs 32: the step's two
       // groups, pair-aligned since G is even; else the element's parity)
       const int n = nt0 + r < p.N ? nt0 + r : p.N - 1;
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
       u32x4 a[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        a[mt] = *reinterpret_cast<const u32x4*>(xb + x_lds_off(mt * 32 + col, 4 * h + j));
+        a[mt] = *reinterpret_cast<const u32x4*>(xb + x_lds_off((wm * MT + mt) * 32 + col, 4 * h + j));
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const u32x4 bw = u32x4{bop[nt][4 * j], bop[nt][4 * j + 1], bop[nt][4 * j + 2], bop[nt][4 * j + 3]};
@@ -321,13 +327,13 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmParams p) {
   auto store = [&](auto put) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int n = nt0 + (wave * NT + nt) * 32 + col;
+      const int n = nt0 + (wn * NT + nt) * 32 + col;
       if (n >= p.N) continue;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          const int m = m0 + (wm * MT + mt) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
           if (m < M) put(m, n, acc[mt][nt][i]);
         }
     }
@@ -353,13 +359,36 @@ __global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __re
 // ---------------------------------------------------------------------------
 QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   QmmConfig c{};
-  c.MT = M > 128 ? 8 : 4;
-  if (const char* env = getenv("LISAQ_QMM_MT")) {
+  // Row tile: 128, 192 or 256 rows (four waves, MT 32-row tiles each), the
+  // one with the least (rounds of 256 workgroups) x (rows per tile), i.e.
+  // the least matrix-core time including the last, partly filled round;
+  // ties go to the taller tile (less W re-reading).
+  c.WM = 1;
+  {
+    const int64_t gn = (N + 255) / 256;
+    int64_t best = -1;
+    for (int mt : {8, 6, 4}) {
+      const int64_t tiles = gn * ((M + 32 * mt - 1) / (32 * mt));
+      const int64_t cost = (tiles + 255) / 256 * 32 * mt;
+      if (best < 0 || cost < best) {
+        best = cost;
+        c.MT = mt;
+      }
+    }
+  }
+  if (const char* env = getenv("LISAQ_QMM_MT")) {  // tuning: 4, 6, 8 (four waves) or 42 (4 x 2 waves)
     const int v = atoi(env);
-    if (v == 4 || v == 8) c.MT = v;
+    if (v == 4 || v == 6 || v == 8) {
+      c.MT = v;
+      c.WM = 1;
+    }
+    if (v == 42) {
+      c.MT = 4;
+      c.WM = 2;
+    }
   }
   c.NT = 2;
-  c.BM = 32 * c.MT;
+  c.BM = 32 * c.MT * c.WM;
   c.BN = 128 * c.NT;
   c.grid_n = (int)((N + c.BN - 1) / c.BN);
   c.grid_m = (int)((M + c.BM - 1) / c.BM);
@@ -388,35 +417,47 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
 
 typedef void (*qmm_fn)(QmmParams);
 
-static int qmm_lds_bytes(int MT, int bits, int gs) {
+static int qmm_lds_bytes(int MT, int WM, int bits, int gs) {
   auto pick = [&](auto l) { return decltype(l)::TOTAL; };
-  if (MT == 8) {
-    if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 8, 2>{}) : pick(QmmLds<4, 64, 8, 2>{});
-    return gs == 32 ? pick(QmmLds<2, 32, 8, 2>{}) : pick(QmmLds<2, 64, 8, 2>{});
+  const int rows = MT * WM;  // 32-row tiles per workgroup: 4, 6 or 8
+  if (rows == 6) {
+    if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 6, 2, 1>{}) : pick(QmmLds<4, 64, 6, 2, 1>{});
+    return gs == 32 ? pick(QmmLds<2, 32, 6, 2, 1>{}) : pick(QmmLds<2, 64, 6, 2, 1>{});
   }
-  if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 4, 2>{}) : pick(QmmLds<4, 64, 4, 2>{});
-  return gs == 32 ? pick(QmmLds<2, 32, 4, 2>{}) : pick(QmmLds<2, 64, 4, 2>{});
+  if (rows == 8) {
+    if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 8, 2, 1>{}) : pick(QmmLds<4, 64, 8, 2, 1>{});
+    return gs == 32 ? pick(QmmLds<2, 32, 8, 2, 1>{}) : pick(QmmLds<2, 64, 8, 2, 1>{});
+  }
+  if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 4, 2, 1>{}) : pick(QmmLds<4, 64, 4, 2, 1>{});
+  return gs == 32 ? pick(QmmLds<2, 32, 4, 2, 1>{}) : pick(QmmLds<2, 64, 4, 2, 1>{});
 }
 
-template <int MT, bool SPLIT>
+template <int MT, int WM, bool SPLIT>
 static qmm_fn qmm_kernel_for(int bits, int gs) {
-  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, MT, 2, SPLIT>;
-  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, MT, 2, SPLIT>;
-  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, MT, 2, SPLIT>;
-  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, MT, 2, SPLIT>;
-  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, MT, 2, SPLIT>;
-  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, MT, 2, SPLIT>;
+  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, MT, 2, WM, SPLIT>;
+  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, MT, 2, WM, SPLIT>;
+  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, MT, 2, WM, SPLIT>;
+  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, MT, 2, WM, SPLIT>;
+  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, MT, 2, WM, SPLIT>;
+  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, MT, 2, WM, SPLIT>;
   return nullptr;
+}
+
+template <bool SPLIT>
+static qmm_fn qmm_pick(const QmmConfig& c, int bits, int gs) {
+  if (c.MT == 8) return qmm_kernel_for<8, 1, SPLIT>(bits, gs);
+  if (c.MT == 6) return qmm_kernel_for<6, 1, SPLIT>(bits, gs);
+  if (c.WM == 2) return qmm_kernel_for<4, 2, SPLIT>(bits, gs);
+  return qmm_kernel_for<4, 1, SPLIT>(bits, gs);
 }
 
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
                int grid_y, void* ws, size_t ws_bytes) {
   // split over K only for plain launches with room for the partials
   const bool split = !p.tiles && c.S > 1 && ws != nullptr && ws_bytes >= c.ws_bytes;
-  qmm_fn fn = c.MT == 8 ? (split ? qmm_kernel_for<8, true>(bits, gs) : qmm_kernel_for<8, false>(bits, gs))
-                        : (split ? qmm_kernel_for<4, true>(bits, gs) : qmm_kernel_for<4, false>(bits, gs));
+  qmm_fn fn = split ? qmm_pick<true>(c, bits, gs) : qmm_pick<false>(c, bits, gs);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);
-  const int lds = qmm_lds_bytes(c.MT, bits, gs);
+  const int lds = qmm_lds_bytes(c.MT, c.WM, bits, gs);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmm: LDS %d bytes: %s", lds, hipGetErrorString(e));
@@ -424,7 +465,7 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
   LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
   p.ksplit = split ? c.S : 1;
   p.partial = split ? static_cast<float*>(ws) : nullptr;
-  hipLaunchKernelGGL(fn, dim3(split ? grid_x * c.S : grid_x, grid_y), dim3(256), lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(split ? grid_x * c.S : grid_x, grid_y), dim3(256 * c.WM), lds, stream, p);
   int rc = check_launch("qmm");
   if (rc || !split) return rc;
   const int64_t MN = (int64_t)p.M * p.N;
