@@ -17,7 +17,7 @@ struct QmmParams {
 };
 
 struct QmmConfig {
-  int MT, NT, WM, BM, BN, grid_n, grid_m;  // WM: waves along M (1 or 2)
+  int MT, NT, WN, BM, BN, grid_n, grid_m;  // WN: waves along N (4 or 8), NT = 8 / WN
   int grid;  // workgroups of a plain (no tile table) launch: grid_n * grid_m
   int S;            // K splits of a plain launch (1: none)
   size_t ws_bytes;  // workspace for the split partials (0 when S == 1)

@@ -22,6 +22,7 @@
 #include "qmm.h"
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 namespace lisaq {
 
@@ -70,6 +71,16 @@ __device__ __forceinline__ void deq2(uint32_t w, float s, float b, uint32_t* o) 
   o[7] = pk_bf16(fmaf(s, ubyte_f32<3>(c2), b), fmaf(s, ubyte_f32<3>(c3), b));
 }
 
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N-1>{})
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <int BITS>
 struct MGeo {
   static constexpr int PACK = 32 / BITS;
@@ -79,14 +90,21 @@ struct MGeo {
 constexpr int BK = 64;
 // x tile in LDS: rows of 64 bf16 (128 B) written by direct-to-LDS loads, one
 // wave instruction = 8 rows = 1 KB.  The 16-byte chunks of a row are XOR-
-// swizzled by (row % 8) and each 8-row group is followed by 16 bytes of
-// padding, so the A-operand reads (32 rows, one chunk each) hit distinct banks.
-constexpr int XG = 1024 + 16;  // bytes per 8-row group
-constexpr int NBUF = 3;        // LDS ring: step k+2 lands while step k runs
+// swizzled by (row % 8) ^ (row / 8 % 2): an A-operand read (lanes 0-31 on
+// rows 0-31, one logical chunk) then puts any 8 consecutive lanes on 8
+// distinct 16-byte bank groups of a 128-byte line and any 16 consecutive lanes
+// on 16 distinct ones of a 256-byte line, i.e. no bank conflicts whether the
+// LDS serves 8 or 16 lanes of a 128-bit read per clock.
+constexpr int XG = 1024;  // bytes per 8-row group
+constexpr int NBUF = 3;   // LDS ring: step k+2 lands while step k runs
 
-__device__ __forceinline__ int x_lds_off(int row, int chunk) {
-  return (row >> 3) * XG + (row & 7) * 128 + ((chunk ^ (row & 7)) << 4);
-}
+__device__ __forceinline__ int x_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int x_lds_off(int row, int chunk) { return row * 128 + ((chunk ^ x_swz(row)) << 4); }
+// Packed W tile (4-bit: 32 bytes = two 16-byte halves per row and K-step):
+// the halves of a row swap when bit 2 ^ bit 3 of the row is set, so the
+// B-operand reads (lanes on 32 consecutive rows, one half) are conflict-free
+// in the same sense.
+__device__ __forceinline__ int w_swz(int row) { return ((row >> 2) ^ (row >> 3)) & 1; }
 
 // 16 / 4 / 2 bytes per lane from global memory straight into LDS (lane l
 // writes lds + size*l; lds must be wave-uniform).
@@ -108,9 +126,23 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
-template <int BITS, int GS, int MT, int NT, int WM>
+// s_waitcnt lgkmcnt(0) (vmcnt, expcnt left alone)
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier without the memory fence of __syncthreads(): the fence
+// would wait for every outstanding global load, including the direct-to-LDS
+// copies just issued for later steps; the waits above say exactly which
+// copies must have landed.  The scheduling barriers keep LDS reads on their
+// side of it.
+__device__ __forceinline__ void block_sync() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BITS, int GS, int MT, int NT, int WN>
 struct QmmLds {
-  static constexpr int BM = 32 * MT * WM, BN = 4 * 32 * NT;
+  static constexpr int BM = 32 * MT, BN = WN * 32 * NT;
   static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
   static constexpr int X = BM / 8 * XG;            // x tile
   static constexpr int W = BN * RB;                // packed W tile
@@ -120,20 +152,23 @@ struct QmmLds {
   static constexpr int TOTAL = NBUF * (X + WSTAGE);
 };
 
-// WM waves along M (1: four waves, each BM rows x 32*NT columns, one wave
-// per SIMD; 2: eight waves, two per SIMD, each half of the rows).
-template <int BITS, int GS, int MT, int NT, int WM, bool SPLIT>
-__global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
+// WN waves side by side along N, each all BM rows x 32*NT columns: four
+// waves (one per SIMD, NT = 2, 256 accumulator registers) or eight (two per
+// SIMD, NT = 1, 128 accumulator registers: a SIMD's second wave fills the
+// matrix-core bubbles of the first).  Either way every W element is
+// dequantized once per workgroup.
+template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT>
+__global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
-  using L = QmmLds<BITS, GS, MT, NT, WM>;
+  using L = QmmLds<BITS, GS, MT, NT, WN>;
   constexpr int BM = L::BM;
   constexpr int BN = L::BN;
-  constexpr int NWV = 4 * WM;  // waves per workgroup
+  constexpr int NWV = WN;  // waves per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int wn = wave & 3, wm = wave >> 2;  // column group, row half
+  const int wn = wave;  // column group
   const int col = lane & 31;
   const int h = lane >> 5;
 
@@ -169,15 +204,16 @@ __global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
   // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
   // matrix are clamped to the last one, their results are never stored)
   // x: BM/8 instructions of 1 KB, XI per wave; lane l fills row 8g + l/8,
-  // physical chunk l%8 (= logical chunk (l%8) ^ (row%8))
+  // physical chunk l%8 (= logical chunk (l%8) ^ x_swz(row), and x_swz(row) =
+  // l/8 ^ (g % 2))
   constexpr int XI = BM / 8 / NWV;
   // element offsets, recomputed per copy to save registers (the host checks
-  // that x fits 2^31 elements); the chunk swizzle uses row % 8 = lane / 8
+  // that x fits 2^31 elements)
   const int xrow0 = m0 + wave * XI * 8 + (lane >> 3);
   const uint32_t xchunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 3);
   auto xoff = [&](int i) -> uint32_t {
     const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
-    return (uint32_t)row * (uint32_t)p.K + xchunk;
+    return (uint32_t)row * (uint32_t)p.K + (xchunk ^ (((wave * XI + i) & 1) << 3));
   };
   // W: BN rows x RB bytes, row-major; 16 bytes per lane: WB bytes per wave in
   // WI instructions (the last lanes idle when a wave's share is under 1 KB)
@@ -192,7 +228,10 @@ __global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
     const int off = wave * WB + i * 1024 + lane * 16;  // byte in the W tile
     int n = nt0 + off / L::RB;
     n = n < p.N ? n : p.N - 1;
-    wsrc[i] = reinterpret_cast<const unsigned char*>(w) + n * rowbytes + off % L::RB;
+    // 4-bit: physical half (off / 16) % 2 of tile row off / 32 holds logical
+    // half ^ w_swz(row)
+    const int lb = BITS == 4 ? (off % L::RB) ^ (w_swz(off / L::RB) << 4) : off % L::RB;
+    wsrc[i] = reinterpret_cast<const unsigned char*>(w) + n * rowbytes + lb;
   }
   // scales / biases: per row the 4-byte-aligned bf16 pair holding the step's
   // group(s); 64 rows per instruction (BN/64 instructions per array, spread
@@ -201,37 +240,41 @@ __global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
   constexpr int SBI = SI * 2 / NWV;            // scale/bias instructions per wave
   static_assert(SBI >= 1 && SI * 2 % NWV == 0, "scale tile geometry");
   constexpr int VM_X = XI, VM_W = WI + SBI;    // DMA instructions per wave: x tile, W stage
-  auto issue_x = [&](int k, int stage) {
+  // copies i0 <= i < i1 of the x tile (i0, i1 compile-time after inlining)
+  auto issue_x = [&](int k, int stage, int i0, int i1) {
     unsigned char* st = smem + stage * L::X;
     const int k0 = k * BK;
 #pragma unroll
-    for (int i = 0; i < XI; ++i) load_lds16(x + xoff(i) + k0, st + (wave * XI + i) * XG);
+    for (int i = 0; i < XI; ++i)
+      if (i >= i0 && i < i1) load_lds16(x + xoff(i) + k0, st + (wave * XI + i) * XG);
   };
-  auto issue_w = [&](int k, int stage) {
+  // copy q of the W stage of step k: q < WI packed W, else scale/bias copy q - WI
+  auto issue_w_part = [&](int k, int stage, int q) {
     unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
     const int k0 = k * BK;
-#pragma unroll
-    for (int i = 0; i < WI; ++i)
-      if (WLANES == 64 || lane < WLANES) load_lds16(wsrc[i] + (int64_t)k0 * BITS / 8, st + wave * WB + i * 1024);
-    // 2*SI scale/bias instructions over the waves
-    const int g = k0 / GS;
-#pragma unroll
-    for (int i = 0; i < SBI; ++i) {
-      const int idx = wave + NWV * i;  // 0 .. 2*SI-1: s row blocks, then b row blocks
-      const bool is_b = idx >= SI;
-      const int blk = is_b ? idx - SI : idx;
-      // (lanes of this instruction load rows blk*64 + lane)
-      const int64_t roff = (int64_t)(nt0 + blk * 64 + lane < p.N ? nt0 + blk * 64 + lane : p.N - 1) * p.G + g;
-      const uint16_t* src = (is_b ? bi : sc) + (roff & ~(int64_t)1);  // (G is even: 4-byte aligned)
-      load_lds4(src, st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
+    if (q < WI) {
+      if (WLANES == 64 || lane < WLANES) load_lds16(wsrc[q] + (int64_t)k0 * BITS / 8, st + wave * WB + q * 1024);
+      return;
     }
+    const int g = k0 / GS;
+    const int idx = wave + NWV * (q - WI);  // 0 .. 2*SI-1: s row blocks, then b row blocks
+    const bool is_b = idx >= SI;
+    const int blk = is_b ? idx - SI : idx;
+    // (lanes of this instruction load rows blk*64 + lane)
+    const int64_t roff = (int64_t)(nt0 + blk * 64 + lane < p.N ? nt0 + blk * 64 + lane : p.N - 1) * p.G + g;
+    const uint16_t* src = (is_b ? bi : sc) + (roff & ~(int64_t)1);  // (G is even: 4-byte aligned)
+    load_lds4(src, st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
+  };
+  auto issue_w = [&](int k, int stage) {
+#pragma unroll
+    for (int q = 0; q < WI + SBI; ++q) issue_w_part(k, stage, q);
   };
 
   // ---- one K-step's W of this lane (LDS stage): packed words, scale, bias
   typedef typename std::conditional<G::WPL == 4, u32x4, u32x2>::type WV;
   struct WLane {
     WV w[NT];
-    float s[NT], b[NT];
+    uint16_t s[NT], b[NT];  // raw bf16 bits (converted where used)
   };
   auto read_w = [&](int k, int stage, WLane& o) {
     const unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
@@ -244,18 +287,24 @@ __global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
       const int n = nt0 + r < p.N ? nt0 + r : p.N - 1;
       const int half = GS == 32 ? h : (int)(((int64_t)n * p.G + g0) & 1);
       const int si = r * 4 + half * 2;
-      o.s[nt] = bf2f(*reinterpret_cast<const uint16_t*>(st + L::W + si));
-      o.b[nt] = bf2f(*reinterpret_cast<const uint16_t*>(st + L::W + L::S + si));
-      o.w[nt] = *reinterpret_cast<const WV*>(st + r * L::RB + h * (4 * G::WPL));
+      o.s[nt] = *reinterpret_cast<const uint16_t*>(st + L::W + si);
+      o.b[nt] = *reinterpret_cast<const uint16_t*>(st + L::W + L::S + si);
+      const int hp = BITS == 4 ? h ^ w_swz(r) : h;
+      o.w[nt] = *reinterpret_cast<const WV*>(st + r * L::RB + hp * (4 * G::WPL));
     }
   };
-  // dequantize word jw into the B operands [nt][16] bf16x2
-  auto dequant_word = [&](const WLane& r, int jw, uint32_t (*bop)[16]) {
+  // s, b as f32 for one column tile of a W lane
+  auto sf = [&](const WLane& r, int nt) { return bf2f(r.s[nt]); };
+  auto bf = [&](const WLane& r, int nt) { return bf2f(r.b[nt]); };
+  // dequantize all words of a W lane into B operands [nt][16] bf16x2
+  auto dequant_all = [&](const WLane& r, uint32_t (*bop)[16]) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      if (BITS == 4) deq4(r.w[nt][jw], r.s[nt], r.b[nt], &bop[nt][jw * 4]);
-      else deq2(r.w[nt][jw], r.s[nt], r.b[nt], &bop[nt][jw * 8]);
-    }
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int jw = 0; jw < G::WPL; ++jw) {
+        if (BITS == 4) deq4(r.w[nt][jw], sf(r, nt), bf(r, nt), &bop[nt][jw * 4]);
+        else deq2(r.w[nt][jw], sf(r, nt), bf(r, nt), &bop[nt][jw * 8]);
+      }
   };
 
   f32x16 acc[MT][NT];
@@ -264,61 +313,136 @@ __global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x16{};
 
-  // Pipeline.  Step k reads x stage k % 3 and refills, sub-step by sub-step,
-  // the B operands with step k+1's W (W stage (k+1) % 3, landed a step
-  // earlier); meanwhile the copies of x(k+2) and W(k+3) are in flight.  Copies
-  // past the last step re-read it, so every step issues the same number of
-  // copies and the waits are constants.
+  // Pipeline.  Step k reads x stage k % 3 and its B operands (dequantized
+  // during step k-1), dequantizes step k+1's W (W stage (k+1) % 3, read from
+  // LDS one step earlier) into the other B buffer, and copies x(k+2) and
+  // W(k+3) into the stages freed by step k-1.  Copies past the last step
+  // re-read it, so every step issues the same number of copies and the waits
+  // are constants.
   // K-steps of this workgroup: [kb, kb + nk) (the whole K unless split)
   const int nk_all = p.K / BK;
   const int per = (nk_all + p.ksplit - 1) / p.ksplit;
   const int kb = split * per;
   const int nk = nk_all - kb < per ? nk_all - kb : per;  // (host: every split has >= 1 step)
   auto kc = [&](int k) { return kb + (k < nk ? k : nk - 1); };
-  uint32_t bop[NT][16];
-  issue_x(kc(0), 0);
+  uint32_t bA[NT][16], bB[NT][16];  // B operands of the current / next step
+  issue_x(kc(0), 0, 0, XI);
   issue_w(kc(0), 0);
   issue_w(kc(1), 1);
-  issue_x(kc(1), 1);
+  issue_x(kc(1), 1, 0, XI);
   issue_w(kc(2), 2);
   wait_vm<VM_X + VM_W>();  // x(0), W(0), W(1) landed (this wave's part)
-  __syncthreads();
+  block_sync();
   {
     WLane w0;
     read_w(kc(0), 0, w0);
-#pragma unroll
-    for (int jw = 0; jw < G::WPL; ++jw) dequant_word(w0, jw, bop);
+    dequant_all(w0, bA);
   }
+  auto read_a1 = [&](const unsigned char* xb, int j, int mt) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(xb + x_lds_off(mt * 32 + col, 4 * h + j));
+  };
+  u32x4 a0[MT], a1[MT];
+  WLane wA, wB;  // W of the step after the current one (alternating)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) a0[mt] = read_a1(smem, 0, mt);
+  read_w(kc(1), 1, wA);
 
+  // One step as 4 * MT * NT slots, each one matrix instruction plus its share
+  // of the other work, in program order (scheduling barriers between slots):
+  //  * sub-step j's first MT slots read the A operands of sub-step j+1
+  //    (sub-step 3: of the next step's sub-step 0, after the barrier);
+  //  * the step's copies are spread evenly over sub-steps 0-2, so the texture
+  //    path drains each before the next arrives and the wave never stalls
+  //    issuing one;
+  //  * the dequantization of the next step's W is cut into pieces of one
+  //    bf16 pair (about five VALU ops) spread evenly over all slots, so the
+  //    VALU work hides under the matrix instructions;
+  //  * between sub-steps 2 and 3: wait for x(k+1), W(k+2) and for this
+  //    step's LDS reads, then the workgroup barrier.
+  constexpr int NMF = MT * NT;
+  constexpr int SLOTS = 4 * NMF;
+  constexpr int NCOPY = XI + WI + SBI;               // copies per wave and step
+  constexpr int PPW = BITS == 4 ? 4 : 8;             // dequant pieces per packed word
+  constexpr int NPIECE = NT * G::WPL * PPW;          // dequant pieces per step
+  static_assert(NCOPY <= 3 * NMF && NPIECE <= SLOTS, "slot plan");
   int xs = 0, ws1 = 1;  // x stage of step k, W stage of step k+1
-  for (int kt = 0; kt < nk; ++kt) {
+  auto step = [&](int kt, uint32_t (*bcur)[16], uint32_t (*bnxt)[16], const WLane& wn, WLane& wnn) {
     const int xs2 = xs == 0 ? 2 : xs - 1;    // (k+2) % 3
     const int ws3 = ws1 == 0 ? 2 : ws1 - 1;  // (k+3) % 3 = k % 3
-    issue_x(kc(kt + 2), xs2);
-    issue_w(kc(kt + 3), ws3);
-    WLane wn;
-    read_w(kc(kt + 1), ws1, wn);
+    const int xs1 = xs == 2 ? 0 : xs + 1;    // (k+1) % 3
+    const int ws2 = ws1 == 2 ? 0 : ws1 + 1;  // (k+2) % 3
     const unsigned char* xb = smem + xs * L::X;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4 a[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        a[mt] = *reinterpret_cast<const u32x4*>(xb + x_lds_off((wm * MT + mt) * 32 + col, 4 * h + j));
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const u32x4 bw = u32x4{bop[nt][4 * j], bop[nt][4 * j + 1], bop[nt][4 * j + 2], bop[nt][4 * j + 3]};
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma32x32x16(as_bf16x8(a[mt]), as_bf16x8(bw), acc[mt][nt]);
+    const unsigned char* xb1 = smem + xs1 * L::X;
+    uint32_t lo[NT][G::WPL], hi[NT][G::WPL], c4[NT][G::WPL][4];  // split codes of the words being dequantized
+    static_for<SLOTS>([&](auto SI) {
+      constexpr int sl = decltype(SI)::value;
+      constexpr int j = sl / NMF, i = sl % NMF;
+      constexpr int nt = i / MT, mt = i % MT;
+      if constexpr (i == 0 && j == 3) {
+        wait_lgkm0();
+        wait_vm<VM_X + VM_W>();
+        block_sync();
       }
-      // the B operands of j are consumed: refill them from the next step's word
-      constexpr int JPW = 4 / G::WPL;  // K sub-steps per word
-      if ((j + 1) % JPW == 0) dequant_word(wn, (j + 1) / JPW - 1, bop);
-    }
-    wait_vm<VM_X + VM_W>();  // x(k+1), W(k+2) landed (issued one step ago)
-    __syncthreads();         // ... for every wave; stages of step k are free
-    xs = xs == 2 ? 0 : xs + 1;
-    ws1 = ws1 == 2 ? 0 : ws1 + 1;
+      // matrix instruction
+      {
+        const u32x4 aw = (j & 1) ? a1[mt] : a0[mt];
+        const u32x4 bw = u32x4{bcur[nt][4 * j], bcur[nt][4 * j + 1], bcur[nt][4 * j + 2], bcur[nt][4 * j + 3]};
+        acc[mt][nt] = mfma32x32x16(as_bf16x8(aw), as_bf16x8(bw), acc[mt][nt]);
+      }
+      // the W words of the step after next, first thing after the barrier (the
+      // next step's first dequantization piece needs them)
+      if constexpr (j == 3 && i == 0) read_w(kc(kt + 2), ws2, wnn);
+      // A operands of the next sub-step
+      if constexpr (i < MT) {
+        if constexpr (j == 0) a1[i] = read_a1(xb, 1, i);
+        if constexpr (j == 1) a0[i] = read_a1(xb, 2, i);
+        if constexpr (j == 2) a1[i] = read_a1(xb, 3, i);
+        if constexpr (j == 3) a0[i] = read_a1(xb1, 0, i);
+      }
+
+      // copies: copy q at slot q * (3 NMF) / NCOPY
+      static_for<NCOPY>([&](auto QI) {
+        constexpr int q = decltype(QI)::value;
+        if constexpr (q * 3 * NMF / NCOPY == sl) {
+          if constexpr (q < XI) issue_x(kc(kt + 2), xs2, q, q + 1);
+          else issue_w_part(kc(kt + 3), ws3, q - XI);
+        }
+      });
+      // dequant pieces: piece d at slot d * SLOTS / NPIECE
+      static_for<NPIECE>([&](auto DI) {
+        constexpr int d = decltype(DI)::value;
+        if constexpr (d * SLOTS / NPIECE == sl) {
+          constexpr int dnt = d / (G::WPL * PPW), dw = d / PPW % G::WPL, dp = d % PPW;
+          const uint32_t wv = wn.w[dnt][dw];
+          const float s_ = sf(wn, dnt), b_ = bf(wn, dnt);
+          if constexpr (BITS == 4) {
+            if constexpr (dp == 0) {
+              lo[dnt][dw] = wv & 0x0F0F0F0Fu;
+              hi[dnt][dw] = (wv >> 4) & 0x0F0F0F0Fu;
+            }
+            bnxt[dnt][dw * 4 + dp] = pk_bf16(fmaf(s_, ubyte_f32<dp>(lo[dnt][dw]), b_), fmaf(s_, ubyte_f32<dp>(hi[dnt][dw]), b_));
+          } else {
+            if constexpr (dp == 0) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) c4[dnt][dw][c] = (wv >> (2 * c)) & 0x03030303u;
+            }
+            constexpr int m = dp / 2, e = (dp % 2) * 2;
+            bnxt[dnt][dw * 8 + dp] = pk_bf16(fmaf(s_, ubyte_f32<m>(c4[dnt][dw][e]), b_), fmaf(s_, ubyte_f32<m>(c4[dnt][dw][e + 1]), b_));
+          }
+        }
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    xs = xs1;
+    ws1 = ws2;
+  };
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, bA, bB, wA, wB);
+    step(kt + 1, bB, bA, wB, wA);
+  }
+  if (kt < nk) {
+    step(kt, bA, bB, wA, wB);
   }
 
   // epilogue: D[m][n], lane holds n = col, rows 8*(i/4) + 4*h + (i%4); a
@@ -333,7 +457,7 @@ __global__ __launch_bounds__(256 * WM) void qmm_kernel(QmmParams p) {
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int m = m0 + (wm * MT + mt) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
           if (m < M) put(m, n, acc[mt][nt][i]);
         }
     }
@@ -359,11 +483,10 @@ __global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __re
 // ---------------------------------------------------------------------------
 QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   QmmConfig c{};
-  // Row tile: 128, 192 or 256 rows (four waves, MT 32-row tiles each), the
-  // one with the least (rounds of 256 workgroups) x (rows per tile), i.e.
-  // the least matrix-core time including the last, partly filled round;
-  // ties go to the taller tile (less W re-reading).
-  c.WM = 1;
+  // Row tile: 128, 192 or 256 rows (MT 32-row tiles), the one with the least
+  // (rounds of 256 workgroups) x (rows per tile), i.e. the least matrix-core
+  // time including the last, partly filled round; ties go to the taller tile
+  // (less W re-reading).  Column tile: 256 (eight waves of 32 columns).
   {
     const int64_t gn = (N + 255) / 256;
     int64_t best = -1;
@@ -376,20 +499,18 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
       }
     }
   }
-  if (const char* env = getenv("LISAQ_QMM_MT")) {  // tuning: 4, 6, 8 (four waves) or 42 (4 x 2 waves)
+  c.WN = 8;
+  if (const char* env = getenv("LISAQ_QMM_MT")) {  // tuning: 4, 6, 8
     const int v = atoi(env);
-    if (v == 4 || v == 6 || v == 8) {
-      c.MT = v;
-      c.WM = 1;
-    }
-    if (v == 42) {
-      c.MT = 4;
-      c.WM = 2;
-    }
+    if (v == 4 || v == 6 || v == 8) c.MT = v;
   }
-  c.NT = 2;
-  c.BM = 32 * c.MT * c.WM;
-  c.BN = 128 * c.NT;
+  if (const char* env = getenv("LISAQ_QMM_WN")) {  // tuning: 4 (NT 2) or 8 (NT 1) waves
+    const int v = atoi(env);
+    if (v == 4 || v == 8) c.WN = v;
+  }
+  c.NT = 8 / c.WN;
+  c.BM = 32 * c.MT;
+  c.BN = 32 * c.NT * c.WN;
   c.grid_n = (int)((N + c.BN - 1) / c.BN);
   c.grid_m = (int)((M + c.BM - 1) / c.BM);
   c.grid = c.grid_n * c.grid_m;  // 1-D launch (see the kernel's tile order)
@@ -409,7 +530,6 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
     c.S = (nk + per - 1) / per;  // every split non-empty
   }
   c.ws_bytes = c.S > 1 ? (size_t)c.S * M * N * 4 : 0;
-  (void)K;
   (void)gs;
   (void)bits;
   return c;
@@ -417,47 +537,38 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
 
 typedef void (*qmm_fn)(QmmParams);
 
-static int qmm_lds_bytes(int MT, int WM, int bits, int gs) {
-  auto pick = [&](auto l) { return decltype(l)::TOTAL; };
-  const int rows = MT * WM;  // 32-row tiles per workgroup: 4, 6 or 8
-  if (rows == 6) {
-    if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 6, 2, 1>{}) : pick(QmmLds<4, 64, 6, 2, 1>{});
-    return gs == 32 ? pick(QmmLds<2, 32, 6, 2, 1>{}) : pick(QmmLds<2, 64, 6, 2, 1>{});
-  }
-  if (rows == 8) {
-    if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 8, 2, 1>{}) : pick(QmmLds<4, 64, 8, 2, 1>{});
-    return gs == 32 ? pick(QmmLds<2, 32, 8, 2, 1>{}) : pick(QmmLds<2, 64, 8, 2, 1>{});
-  }
-  if (bits == 4) return gs == 32 ? pick(QmmLds<4, 32, 4, 2, 1>{}) : pick(QmmLds<4, 64, 4, 2, 1>{});
-  return gs == 32 ? pick(QmmLds<2, 32, 4, 2, 1>{}) : pick(QmmLds<2, 64, 4, 2, 1>{});
-}
-
-template <int MT, int WM, bool SPLIT>
-static qmm_fn qmm_kernel_for(int bits, int gs) {
-  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, MT, 2, WM, SPLIT>;
-  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, MT, 2, WM, SPLIT>;
-  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, MT, 2, WM, SPLIT>;
-  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, MT, 2, WM, SPLIT>;
-  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, MT, 2, WM, SPLIT>;
-  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, MT, 2, WM, SPLIT>;
+template <int MT, int WN, bool SPLIT>
+static qmm_fn qmm_kernel_for(int bits, int gs, int* lds) {
+  constexpr int NT = 8 / WN;
+  *lds = bits == 4 ? QmmLds<4, 64, MT, NT, WN>::TOTAL : QmmLds<2, 64, MT, NT, WN>::TOTAL;  // (gs-independent)
+  if (bits == 4 && gs == 64) return qmm_kernel<4, 64, MT, NT, WN, SPLIT>;
+  if (bits == 4 && gs == 32) return qmm_kernel<4, 32, MT, NT, WN, SPLIT>;
+  if (bits == 4 && gs == 128) return qmm_kernel<4, 128, MT, NT, WN, SPLIT>;
+  if (bits == 2 && gs == 64) return qmm_kernel<2, 64, MT, NT, WN, SPLIT>;
+  if (bits == 2 && gs == 32) return qmm_kernel<2, 32, MT, NT, WN, SPLIT>;
+  if (bits == 2 && gs == 128) return qmm_kernel<2, 128, MT, NT, WN, SPLIT>;
   return nullptr;
 }
 
+template <int WN, bool SPLIT>
+static qmm_fn qmm_pick_mt(const QmmConfig& c, int bits, int gs, int* lds) {
+  if (c.MT == 8) return qmm_kernel_for<8, WN, SPLIT>(bits, gs, lds);
+  if (c.MT == 6) return qmm_kernel_for<6, WN, SPLIT>(bits, gs, lds);
+  return qmm_kernel_for<4, WN, SPLIT>(bits, gs, lds);
+}
+
 template <bool SPLIT>
-static qmm_fn qmm_pick(const QmmConfig& c, int bits, int gs) {
-  if (c.MT == 8) return qmm_kernel_for<8, 1, SPLIT>(bits, gs);
-  if (c.MT == 6) return qmm_kernel_for<6, 1, SPLIT>(bits, gs);
-  if (c.WM == 2) return qmm_kernel_for<4, 2, SPLIT>(bits, gs);
-  return qmm_kernel_for<4, 1, SPLIT>(bits, gs);
+static qmm_fn qmm_pick(const QmmConfig& c, int bits, int gs, int* lds) {
+  return c.WN == 8 ? qmm_pick_mt<8, SPLIT>(c, bits, gs, lds) : qmm_pick_mt<4, SPLIT>(c, bits, gs, lds);
 }
 
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
                int grid_y, void* ws, size_t ws_bytes) {
   // split over K only for plain launches with room for the partials
   const bool split = !p.tiles && c.S > 1 && ws != nullptr && ws_bytes >= c.ws_bytes;
-  qmm_fn fn = split ? qmm_pick<true>(c, bits, gs) : qmm_pick<false>(c, bits, gs);
+  int lds = 0;
+  qmm_fn fn = split ? qmm_pick<true>(c, bits, gs, &lds) : qmm_pick<false>(c, bits, gs, &lds);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);
-  const int lds = qmm_lds_bytes(c.MT, c.WM, bits, gs);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmm: LDS %d bytes: %s", lds, hipGetErrorString(e));
@@ -465,7 +576,7 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
   LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
   p.ksplit = split ? c.S : 1;
   p.partial = split ? static_cast<float*>(ws) : nullptr;
-  hipLaunchKernelGGL(fn, dim3(split ? grid_x * c.S : grid_x, grid_y), dim3(256 * c.WM), lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(split ? grid_x * c.S : grid_x, grid_y), dim3(64 * c.WN), lds, stream, p);
   int rc = check_launch("qmm");
   if (rc || !split) return rc;
   const int64_t MN = (int64_t)p.M * p.N;
