@@ -33,22 +33,23 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Byte i of a word as f32 (v_cvt_f32_ubyte<i>: one instruction; written out
-// because the compiler turns masked nibble fields into v_bfe + ubyte0).
+// Byte I of a word as f32: one v_cvt_f32_ubyte<I>.
 template <int I>
 __device__ __forceinline__ float ubyte_f32(uint32_t v) {
-  float r;
-  if constexpr (I == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (I == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (I == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-  return r;
+  return (float)((v >> (8 * I)) & 0xFFu);
+}
+// A word of masked codes made opaque to the optimizer, which would otherwise
+// fold the mask into each byte extraction (v_bfe + v_cvt_f32_ubyte0 instead
+// of one v_cvt_f32_ubyte<I>).
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 // Dequantize the 8 codes of one u32 (4-bit) into 4 bf16x2 in natural K order.
 __device__ __forceinline__ void deq4(uint32_t w, float s, float b, uint32_t* o) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;         // codes 0,2,4,6
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
+  const uint32_t lo = opaque(w & 0x0F0F0F0Fu);         // codes 0,2,4,6
+  const uint32_t hi = opaque((w >> 4) & 0x0F0F0F0Fu);  // codes 1,3,5,7
   o[0] = pk_bf16(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
   o[1] = pk_bf16(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
   o[2] = pk_bf16(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
@@ -57,10 +58,10 @@ __device__ __forceinline__ void deq4(uint32_t w, float s, float b, uint32_t* o) 
 
 // Dequantize the 16 codes of one u32 (2-bit) into 8 bf16x2 in natural K order.
 __device__ __forceinline__ void deq2(uint32_t w, float s, float b, uint32_t* o) {
-  const uint32_t c0 = w & 0x03030303u;         // codes 0,4,8,12
-  const uint32_t c1 = (w >> 2) & 0x03030303u;  // codes 1,5,9,13
-  const uint32_t c2 = (w >> 4) & 0x03030303u;  // codes 2,6,10,14
-  const uint32_t c3 = (w >> 6) & 0x03030303u;  // codes 3,7,11,15
+  const uint32_t c0 = opaque(w & 0x03030303u);         // codes 0,4,8,12
+  const uint32_t c1 = opaque((w >> 2) & 0x03030303u);  // codes 1,5,9,13
+  const uint32_t c2 = opaque((w >> 4) & 0x03030303u);  // codes 2,6,10,14
+  const uint32_t c3 = opaque((w >> 6) & 0x03030303u);  // codes 3,7,11,15
   o[0] = pk_bf16(fmaf(s, ubyte_f32<0>(c0), b), fmaf(s, ubyte_f32<0>(c1), b));
   o[1] = pk_bf16(fmaf(s, ubyte_f32<0>(c2), b), fmaf(s, ubyte_f32<0>(c3), b));
   o[2] = pk_bf16(fmaf(s, ubyte_f32<1>(c0), b), fmaf(s, ubyte_f32<1>(c1), b));
@@ -383,22 +384,31 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
         wait_vm<VM_X + VM_W>();
         block_sync();
       }
-      // matrix instruction
+      // matrix instruction (issued before the slot's LDS reads, so its operand
+      // wait does not also wait for them)
       {
         const u32x4 aw = (j & 1) ? a1[mt] : a0[mt];
         const u32x4 bw = u32x4{bcur[nt][4 * j], bcur[nt][4 * j + 1], bcur[nt][4 * j + 2], bcur[nt][4 * j + 3]};
-        acc[mt][nt] = mfma32x32x16(as_bf16x8(aw), as_bf16x8(bw), acc[mt][nt]);
+        // W as the row operand, x as the column operand: the accumulator is
+        // y^T, so a lane holds runs of 4 consecutive outputs of one row
+        acc[mt][nt] = mfma32x32x16(as_bf16x8(bw), as_bf16x8(aw), acc[mt][nt]);
       }
+      __builtin_amdgcn_sched_barrier(0);
       // the W words of the step after next, first thing after the barrier (the
       // next step's first dequantization piece needs them)
       if constexpr (j == 3 && i == 0) read_w(kc(kt + 2), ws2, wnn);
-      // A operands of the next sub-step
-      if constexpr (i < MT) {
-        if constexpr (j == 0) a1[i] = read_a1(xb, 1, i);
-        if constexpr (j == 1) a0[i] = read_a1(xb, 2, i);
-        if constexpr (j == 2) a1[i] = read_a1(xb, 3, i);
-        if constexpr (j == 3) a0[i] = read_a1(xb1, 0, i);
-      }
+      // A operands of the next sub-step, two per slot in the sub-step's first
+      // slots: they have landed by the sub-step's end (where the compiler
+      // waits for all outstanding LDS reads)
+      static_for<2>([&](auto RI) {
+        constexpr int r = 2 * i + decltype(RI)::value;
+        if constexpr (r < MT) {
+          if constexpr (j == 0) a1[r] = read_a1(xb, 1, r);
+          if constexpr (j == 1) a0[r] = read_a1(xb, 2, r);
+          if constexpr (j == 2) a1[r] = read_a1(xb, 3, r);
+          if constexpr (j == 3) a0[r] = read_a1(xb1, 0, r);
+        }
+      });
 
       // copies: copy q at slot q * (3 NMF) / NCOPY
       static_for<NCOPY>([&](auto QI) {
@@ -417,14 +427,14 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
           const float s_ = sf(wn, dnt), b_ = bf(wn, dnt);
           if constexpr (BITS == 4) {
             if constexpr (dp == 0) {
-              lo[dnt][dw] = wv & 0x0F0F0F0Fu;
-              hi[dnt][dw] = (wv >> 4) & 0x0F0F0F0Fu;
+              lo[dnt][dw] = opaque(wv & 0x0F0F0F0Fu);
+              hi[dnt][dw] = opaque((wv >> 4) & 0x0F0F0F0Fu);
             }
             bnxt[dnt][dw * 4 + dp] = pk_bf16(fmaf(s_, ubyte_f32<dp>(lo[dnt][dw]), b_), fmaf(s_, ubyte_f32<dp>(hi[dnt][dw]), b_));
           } else {
             if constexpr (dp == 0) {
 #pragma unroll
-              for (int c = 0; c < 4; ++c) c4[dnt][dw][c] = (wv >> (2 * c)) & 0x03030303u;
+              for (int c = 0; c < 4; ++c) c4[dnt][dw][c] = opaque((wv >> (2 * c)) & 0x03030303u);
             }
             constexpr int m = dp / 2, e = (dp % 2) * 2;
             bnxt[dnt][dw * 8 + dp] = pk_bf16(fmaf(s_, ubyte_f32<m>(c4[dnt][dw][e]), b_), fmaf(s_, ubyte_f32<m>(c4[dnt][dw][e + 1]), b_));
@@ -445,28 +455,45 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
     step(kt, bA, bB, wA, wB);
   }
 
-  // epilogue: D[m][n], lane holds n = col, rows 8*(i/4) + 4*h + (i%4); a
-  // split writes its f32 partial instead (one uniform branch around the
-  // whole store loop keeps the accumulators in registers)
-  auto store = [&](auto put) {
+  // epilogue: the accumulator of (mt, nt) is y^T: lane holds row m = col of
+  // the mt tile and columns 8*(i/4) + 4*h + (i%4) of the nt tile, i.e. four
+  // runs of 4 consecutive outputs, stored as one 8-byte (bf16) or 16-byte
+  // (f32 split partial) store each when N % 4 == 0.  A split writes its f32
+  // partial instead (one uniform branch around the whole store loop keeps the
+  // accumulators in registers).
+  const bool vec = (p.N & 3) == 0;
+  auto store = [&](auto put4, auto put1) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int n = nt0 + (wn * NT + nt) * 32 + col;
-      if (n >= p.N) continue;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 32 + col;
+      if (m >= M) continue;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (m < M) put(m, n, acc[mt][nt][i]);
+        for (int g = 0; g < 4; ++g) {
+          const int n = nt0 + (wn * NT + nt) * 32 + 8 * g + 4 * h;
+          const f32x16& a = acc[mt][nt];
+          if (vec && n + 3 < p.N) {
+            put4(m, n, a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) put1(m, n + e, a[4 * g + e]);
+          }
         }
     }
   };
   if constexpr (SPLIT) {
     float* part = p.partial + (int64_t)split * M * p.N;
-    store([&](int m, int n, float v) { part[(int64_t)m * p.N + n] = v; });
+    store([&](int m, int n, float v0, float v1, float v2, float v3) {
+            *reinterpret_cast<f32x4*>(part + (int64_t)m * p.N + n) = f32x4{v0, v1, v2, v3};
+          },
+          [&](int m, int n, float v) { part[(int64_t)m * p.N + n] = v; });
   } else {
-    store([&](int m, int n, float v) { y[(int64_t)m * p.N + n] = f2bf(v); });
+    store([&](int m, int n, float v0, float v1, float v2, float v3) {
+            *reinterpret_cast<u32x2*>(y + (int64_t)m * p.N + n) = u32x2{pk_bf16(v0, v1), pk_bf16(v2, v3)};
+          },
+          [&](int m, int n, float v) { y[(int64_t)m * p.N + n] = f2bf(v); });
   }
 }
 

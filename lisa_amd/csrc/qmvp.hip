@@ -298,6 +298,10 @@ QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   }
   c.NW = 4;
   int64_t grid = 256LL * wgs_per_cu;
+  if (const char* env = getenv("LISAQ_QMVP_GRID")) {  // tuning: workgroups
+    const int v = atoi(env);
+    if (v >= 64 && v <= 4096) grid = v;
+  }
   const int64_t need = (N + 3) / 4;
   c.tiles = (int)(grid < need ? grid : need);
   const int64_t waves = 4LL * c.tiles;
