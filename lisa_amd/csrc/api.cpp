@@ -10,6 +10,7 @@
 #include <cstring>
 
 #include "kernels.h"
+#include <cstdlib>
 #include "lisaq_common.h"
 #include "qmm.h"
 #include "qmv.h"
@@ -190,6 +191,10 @@ extern "C" {
 int lisaq_version(void) { return 100; }
 
 const char* lisaq_last_error(void) { return g_err; }
+
+int lisaq_moe_decode_supported(int64_t T, int64_t H, int64_t I, int k, int gs, int bits) {
+  return moe_decode_supported(T, H, I, k, gs, bits) ? 1 : 0;
+}
 
 int lisaq_qmv_batch_limit(int64_t K, int64_t N) {
   if (K <= 2048 && N <= 2048) return 33;
@@ -491,6 +496,17 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   const size_t gws_bytes = L.total - L.gws;
   int rc;
   if ((rc = lisaq_moe_route(st, logits, T, E, k, idx, wts))) return rc;
+  // Few tokens (T <= 8, the reference's decode window): fused path, two
+  // launches after the router (LISAQ_MOE_FUSED=0 selects the generic path)
+  const char* fenv = getenv("LISAQ_MOE_FUSED");
+  if (!(fenv && fenv[0] == '0') && moe_decode_supported(T, H, I, k, gs, bits)) {
+    if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
+    if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
+    if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, out, R, H, I, 1, gs, bits))) return rc;
+    return launch_moe_decode(st, (const uint16_t*)x, idx, wts, gw, (const uint16_t*)gsc, (const uint16_t*)gbi, uw,
+                             (const uint16_t*)usc, (const uint16_t*)ubi, dw, (const uint16_t*)dsc,
+                             (const uint16_t*)dbi, g, (uint16_t*)out, T, H, I, E, k, gs, bits);
+  }
   if ((rc = lisaq_moe_sort(st, idx, R, E, k, sorted, order, rows, inv, offs))) return rc;
   if ((rc = lisaq_gather_rows(st, x, rows, xs, R, H))) return rc;
   // gate and up share one set of tile tables; every run is at most T rows

@@ -7,73 +7,88 @@
 // sort), crates/lisa-mlx/src/shaders/common/exact_header.metal:2-24.
 #include "lisaq_common.h"
 #include "kernels.h"
+#include "moe_dev.h"
 
 namespace lisaq {
 
 // ---------------------------------------------------------------------------
 // Router: one wave per token.  Top-k = the first k of a stable ascending sort
 // of -logits: largest logit first, equal logits in increasing expert order.
-// Each of the k rounds takes the wave-wide (max value, min index) among the
-// experts not yet taken.  Softmax over the k selected logits in f32:
-// e = exp(l - max), w = e * (1/sum) (softmax_single_row's normalizer).
+// Each of the k rounds: every lane takes its best expert not yet chosen
+// (ties: lowest id), the wave maximum comes from a DPP max ladder (no LDS
+// round trips), and the winner is the lowest expert id holding that value,
+// found with one ballot per expert slot.  (A NaN logit counts as -inf.)
+// Softmax over the k selected logits in f32: e = exp(l - max), the sum in
+// round order, w = e * (1/sum) (softmax_single_row's normalizer).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float route_dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY),
+                                                               __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF,
+                                                               false));
+}
+// wave maximum, broadcast (lane 63 collects rows 0..3 through the row
+// broadcasts, then readlane)
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, route_dpp<0xB1, 0xF>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, route_dpp<0x4E, 0xF>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, route_dpp<0x141, 0xF>(v));  // row_half_mirror
+  v = fmaxf(v, route_dpp<0x140, 0xF>(v));  // row_mirror: every lane holds its row's max
+  v = fmaxf(v, route_dpp<0x142, 0xA>(v));  // row_bcast15
+  v = fmaxf(v, route_dpp<0x143, 0xC>(v));  // row_bcast31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+template <int PER>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int64_t T,
                                                     int E, int k, int32_t* __restrict__ idx,
                                                     float* __restrict__ wts) {
   const int lane = threadIdx.x & 63;
   const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  constexpr int PER = 16;  // E <= 1024
   const float* l = logits + t * E;
   float v[PER];
   uint32_t taken = 0;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
-    v[i] = e < E ? l[e] : -INFINITY;
+    const float x = e < E ? l[e] : -INFINITY;
+    v[i] = x != x ? -INFINITY : x + 0.0f;  // NaN -> -inf; -0 -> +0
     if (e >= E) taken |= 1u << i;
   }
-  // lane r keeps round r's winner (k <= 64), so nothing lives in scratch
+  // lane r keeps round r's winner (k <= 64)
   float mysel = -INFINITY;
   int mysid = 0;
   for (int r = 0; r < k; ++r) {
-    float best = 0.f;
-    int bi = 0x7fffffff;
+    // lane-local best not yet taken (scanning upward keeps the lowest slot on ties)
+    float best = -INFINITY;
+    int bslot = -1;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      if (taken & (1u << i)) continue;
-      if (bi == 0x7fffffff || v[i] > best) {  // scanning e upward keeps the lower id on ties
-        best = v[i];
-        bi = e;
-      }
+      const bool ok = !(taken & (1u << i)) && (bslot < 0 || v[i] > best);
+      best = ok ? v[i] : best;
+      bslot = ok ? i : bslot;
     }
+    const float m = wave_max(bslot >= 0 ? best : -INFINITY);
+    // the lowest expert id with value m: lowest slot, then lowest lane
+    int win = -1;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ob = __shfl_xor(best, off);
-      const int oi = __shfl_xor(bi, off);
-      const bool take = (oi != 0x7fffffff) && (bi == 0x7fffffff || ob > best || (!(ob < best) && oi < bi));
-      if (take) {
-        best = ob;
-        bi = oi;
-      }
+    for (int i = 0; i < PER; ++i) {
+      const uint64_t bal = __ballot(bslot == i && best == m);
+      if (win < 0 && bal != 0) win = i * 64 + (int)__builtin_ctzll(bal);
     }
-    if ((bi & 63) == lane && bi != 0x7fffffff) taken |= 1u << (bi >> 6);
+    if (win < 0) win = 0;  // (only when fewer than k experts remain; k <= E is checked on the host)
+    if ((win & 63) == lane) taken |= 1u << (win >> 6);
     if (lane == r) {
-      mysel = best;
-      mysid = bi;
+      mysel = m;
+      mysid = win;
     }
   }
   // softmax over the k selected logits: max, then exp and the sum in round
-  // order (lane 0 adds lanes 1..k-1 in turn), w = e * (1/sum)
-  float mx = mysel;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float o = __shfl_xor(mx, off);
-    mx = mx < o ? o : mx;
-  }
+  // order, w = e * (1/sum)
+  const float mx = wave_max(lane < k ? mysel : -INFINITY);
   const float ex = lane < k ? expf(mysel - mx) : 0.f;
   float sum = 0.f;
-  for (int r = 0; r < k; ++r) sum += __shfl(ex, r);
+  for (int r = 0; r < k; ++r) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
   const float inv = 1.0f / sum;
   if (lane < k) {
     idx[t * k + lane] = mysid;
@@ -84,8 +99,10 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 int launch_route(hipStream_t st, const float* logits, int64_t T, int E, int k, int32_t* idx,
                  float* wts) {
   if (T == 0) return LISAQ_OK;
-  hipLaunchKernelGGL(route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, T, E, k, idx,
-                     wts);
+  const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+  if (E <= 128) hipLaunchKernelGGL(route_kernel<2>, grid, block, 0, st, logits, T, E, k, idx, wts);
+  else if (E <= 256) hipLaunchKernelGGL(route_kernel<4>, grid, block, 0, st, logits, T, E, k, idx, wts);
+  else hipLaunchKernelGGL(route_kernel<16>, grid, block, 0, st, logits, T, E, k, idx, wts);
   return check_launch("moe_route");
 }
 
@@ -218,11 +235,6 @@ int launch_gather_rows(hipStream_t st, const uint16_t* x, const int32_t* rows, u
 // ---------------------------------------------------------------------------
 // act = bf16( bf16(g * bf16(sigmoid(g))) * u ); sigmoid as the MLX unary op:
 // y = 1/(1+exp(|x|)), x<0 ? y : 1-y.
-__device__ __forceinline__ float silu_bf16(float g) {
-  const float y = 1.0f / (1.0f + expf(fabsf(g)));
-  const float sg = bf2f(f2bf(g < 0.0f ? y : 1.0f - y));
-  return bf2f(f2bf(__fmul_rn(g, sg)));
-}
 
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ g,
                                                      const uint16_t* __restrict__ u,

@@ -1,0 +1,301 @@
+// Fused decode MoE (few tokens): gate|up matvec + SwiGLU in one launch, down
+// matvec + weighted combine in another, after the router.
+//
+// Reference: the engine's one-token decode MoE, track_moe_route_1 ->
+// track_moe_gate_up_reuse_2row -> track_moe_down_combine_1
+// (crates/lisa-engine/src/models/qwen4/moe.rs:263-332,
+// crates/lisa-mlx/src/models/qwen4/moe_decode.rs:137-270,
+// crates/lisa-mlx/src/shaders/qwen4/gate_up_act.metal and down_combine.metal).
+// Same rounding points as the generic path (and as the reference kernels):
+// gate and up outputs rounded to bf16, act = bf16(silu(g) * u), each expert's
+// down output rounded to bf16, multiplied by its f32 routing weight, folded in
+// the colsum_small order, rounded once.  The routed-expert part only: the
+// shared expert and its gate are outside this path.
+//
+// MI355X shape.  gate_up_act: one (token, expert) pair per grid row, each wave
+// RPW rows of I; a lane owns the 32-code chunks lane, lane+64, ... of the H
+// inputs, so one 16-byte load per lane and row reads a whole 1 KB row slice
+// and x stays in registers; all RPW rows' loads are issued before any math.
+// down_combine: each wave RPW output rows of H; the k experts of the token are
+// side by side in the wave (64/k lanes per expert row), the partial dot
+// products are summed within each lane group, and the k results are folded
+// in the combine order by one lane.  Matvec arithmetic as the decode qmv:
+// per chunk, s * (sum(x * (128 + q)) - 128 * sum(x)) + b * sum(x) in f32.
+#include "lisaq_common.h"
+#include "kernels.h"
+#include "moe_dev.h"
+#include "qmv_dev.h"
+
+namespace lisaq {
+using namespace qmvdev;
+
+namespace {
+
+struct MoeDecodeParams {
+  const uint16_t* x;    // [T, H] bf16
+  const int32_t* idx;   // [T*k] expert ids in slot order t*k + j
+  const float* wts;     // [T*k] routing weights
+  const uint32_t *gw, *uw, *dw;                 // [E, I, H/pack], [E, I, H/pack], [E, H, I/pack]
+  const uint16_t *gsc, *gbi, *usc, *ubi, *dsc, *dbi;
+  uint16_t* act;        // [T*k, I] bf16
+  uint16_t* out;        // [T, H] bf16
+  int T, H, I, E, k;
+};
+
+constexpr int RPW = 2;  // rows per wave (both kernels)
+
+// one chunk (32 codes) of a W row: 16 bytes at 4 bits, 8 at 2
+template <int BITS>
+__device__ __forceinline__ void load_chunk(const uint32_t* p, uint32_t* w) {
+  if constexpr (BITS == 4) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+  } else {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    w[0] = v[0]; w[1] = v[1];
+  }
+}
+
+// x of one chunk: 32 bf16 = 4 x 16 bytes
+__device__ __forceinline__ void load_x_chunk(const uint16_t* p, uint32_t* raw) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
+    raw[4 * i] = v[0]; raw[4 * i + 1] = v[1]; raw[4 * i + 2] = v[2]; raw[4 * i + 3] = v[3];
+  }
+}
+
+template <int BITS, int GS, int J>
+__global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p) {
+  constexpr int PACK = 32 / BITS, WPC = 32 / PACK;  // words per chunk
+  constexpr int NP = WPC * (16 / BITS);             // pairs per chunk
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int z = blockIdx.y;  // slot t*k + j
+  const int t = z / p.k;
+  const int e = p.idx[z];
+  const bool valid_e = e >= 0 && e < p.E;
+  const int r0 = (blockIdx.x * 4 + wave) * RPW;
+  if (r0 >= p.I) return;
+  const int C = p.H / 32, G = p.H / GS;
+  const int64_t wrow = p.H / PACK;  // words per W row
+  // x of the lane's chunks (paired after every load is in flight)
+  uint32_t raw[J][16];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    if (c < C) load_x_chunk(p.x + (int64_t)t * p.H + c * 32, raw[j]);
+    else
+#pragma unroll
+      for (int i = 0; i < 16; ++i) raw[j][i] = 0;
+  }
+  // every row's W words, scales and biases
+  uint32_t wg_[RPW][J][WPC], wu_[RPW][J][WPC];
+  uint16_t sg_[RPW][J], bg_[RPW][J], su_[RPW][J], bu_[RPW][J];
+  const int64_t ebase = valid_e ? (int64_t)e * p.I : 0;
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int r = r0 + rr < p.I ? r0 + rr : p.I - 1;
+    const int64_t row = ebase + r;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      if (c < C) {
+        load_chunk<BITS>(p.gw + row * wrow + c * WPC, wg_[rr][j]);
+        load_chunk<BITS>(p.uw + row * wrow + c * WPC, wu_[rr][j]);
+        const int64_t si = row * G + c * 32 / GS;
+        sg_[rr][j] = p.gsc[si]; bg_[rr][j] = p.gbi[si];
+        su_[rr][j] = p.usc[si]; bu_[rr][j] = p.ubi[si];
+      } else {
+#pragma unroll
+        for (int i = 0; i < WPC; ++i) wg_[rr][j][i] = wu_[rr][j][i] = 0;
+        sg_[rr][j] = bg_[rr][j] = su_[rr][j] = bu_[rr][j] = 0;
+      }
+    }
+  }
+  uint32_t xp[J][NP];
+  float sx[J], st[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) pair_x<BITS>(raw[j], xp[j], sx[j], st[j]);
+  PConst kc;
+  kc.init();
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    float pg = 0.f, pu = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const float dg = chunk_dot<BITS>(wg_[rr][j], xp[j], kc);
+      const float du = chunk_dot<BITS>(wu_[rr][j], xp[j], kc);
+      pg = fmaf(bf2f(sg_[rr][j]), dg - 128.0f * st[j], fmaf(bf2f(bg_[rr][j]), sx[j], pg));
+      pu = fmaf(bf2f(su_[rr][j]), du - 128.0f * st[j], fmaf(bf2f(bu_[rr][j]), sx[j], pu));
+    }
+    const float g = wave_sum(pg), u = wave_sum(pu);
+    const int r = r0 + rr;
+    if (lane == 0 && r < p.I)
+      p.act[(int64_t)z * p.I + r] = valid_e ? swiglu_bf16(bf2f(f2bf(g)), bf2f(f2bf(u))) : (uint16_t)0;
+  }
+}
+
+// sum over the LPR lanes of each lane group (butterfly, fixed order)
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+template <int BITS, int GS, int KE, int P>
+__global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p) {
+  constexpr int PACK = 32 / BITS, WPC = 32 / PACK;
+  constexpr int NP = WPC * (16 / BITS);
+  constexpr int LPR = 64 / KE;  // lanes per expert row
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.y;
+  const int d0 = (blockIdx.x * 4 + wave) * RPW;
+  if (d0 >= p.H) return;
+  const int jx = lane / LPR, sub = lane % LPR;  // expert slot and lane within its row
+  const int z = t * KE + jx;
+  const int C = p.I / 32, G = p.I / GS;
+  const int64_t wrow = p.I / PACK;
+  // the activations of the lane's chunks first (paired after every load is
+  // in flight), then the expert id and weight
+  uint32_t raw[P][16];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    const int c = sub + LPR * q;
+    if (c < C) load_x_chunk(p.act + (int64_t)z * p.I + c * 32, raw[q]);
+    else
+#pragma unroll
+      for (int i = 0; i < 16; ++i) raw[q][i] = 0;
+  }
+  const int e = p.idx[z];
+  const bool valid_e = e >= 0 && e < p.E;
+  const float wz = p.wts[z];
+  uint32_t w_[RPW][P][WPC];
+  uint16_t s_[RPW][P], b_[RPW][P];
+  const int64_t ebase = valid_e ? (int64_t)e * p.H : 0;
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int d = d0 + rr < p.H ? d0 + rr : p.H - 1;
+    const int64_t row = ebase + d;
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const int c = sub + LPR * q;
+      if (c < C) {
+        load_chunk<BITS>(p.dw + row * wrow + c * WPC, w_[rr][q]);
+        const int64_t si = row * G + c * 32 / GS;
+        s_[rr][q] = p.dsc[si]; b_[rr][q] = p.dbi[si];
+      } else {
+#pragma unroll
+        for (int i = 0; i < WPC; ++i) w_[rr][q][i] = 0;
+        s_[rr][q] = b_[rr][q] = 0;
+      }
+    }
+  }
+  uint32_t xp[P][NP];
+  float sx[P], st[P];
+#pragma unroll
+  for (int q = 0; q < P; ++q) pair_x<BITS>(raw[q], xp[q], sx[q], st[q]);
+  PConst kc;
+  kc.init();
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    float part = 0.f;
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const float dq = chunk_dot<BITS>(w_[rr][q], xp[q], kc);
+      part = fmaf(bf2f(s_[rr][q]), dq - 128.0f * st[q], fmaf(bf2f(b_[rr][q]), sx[q], part));
+    }
+    const float res = group_sum<LPR>(part);  // every lane of the group holds its expert's dot
+    const float prod = valid_e ? __fmul_rn(bf2f(f2bf(res)), wz) : 0.0f;
+    float pr[KE];
+#pragma unroll
+    for (int j = 0; j < KE; ++j) pr[j] = __shfl(prod, j * LPR);
+    const int d = d0 + rr;
+    if (lane == 0 && d < p.H) p.out[(int64_t)t * p.H + d] = f2bf(combine_fold<KE>(pr, KE));
+  }
+}
+
+typedef void (*moe_fn)(MoeDecodeParams);
+
+template <int BITS, int GS>
+moe_fn pick_gu(int J) {
+  if (J == 1) return moe_gate_up_act_kernel<BITS, GS, 1>;
+  if (J == 2) return moe_gate_up_act_kernel<BITS, GS, 2>;
+  if (J == 3) return moe_gate_up_act_kernel<BITS, GS, 3>;
+  if (J == 4) return moe_gate_up_act_kernel<BITS, GS, 4>;
+  return nullptr;
+}
+
+template <int BITS, int GS, int KE>
+moe_fn pick_dc_p(int P) {
+  switch (P) {
+    case 1: return moe_down_combine_kernel<BITS, GS, KE, 1>;
+    case 2: return moe_down_combine_kernel<BITS, GS, KE, 2>;
+    case 3: return moe_down_combine_kernel<BITS, GS, KE, 3>;
+    case 4: return moe_down_combine_kernel<BITS, GS, KE, 4>;
+    case 6: return moe_down_combine_kernel<BITS, GS, KE, 6>;
+    case 8: return moe_down_combine_kernel<BITS, GS, KE, 8>;
+    default: return nullptr;
+  }
+}
+
+template <int BITS, int GS>
+moe_fn pick_dc(int k, int P) {
+  switch (k) {
+    case 1: return pick_dc_p<BITS, GS, 1>(P);
+    case 2: return pick_dc_p<BITS, GS, 2>(P);
+    case 4: return pick_dc_p<BITS, GS, 4>(P);
+    case 8: return pick_dc_p<BITS, GS, 8>(P);
+    case 16: return pick_dc_p<BITS, GS, 16>(P);
+    default: return nullptr;
+  }
+}
+
+template <typename F>
+moe_fn by_format(int bits, int gs, F f) {
+  if (bits == 4 && gs == 32) return f(std::integral_constant<int, 4>{}, std::integral_constant<int, 32>{});
+  if (bits == 4 && gs == 64) return f(std::integral_constant<int, 4>{}, std::integral_constant<int, 64>{});
+  if (bits == 4 && gs == 128) return f(std::integral_constant<int, 4>{}, std::integral_constant<int, 128>{});
+  if (bits == 2 && gs == 32) return f(std::integral_constant<int, 2>{}, std::integral_constant<int, 32>{});
+  if (bits == 2 && gs == 64) return f(std::integral_constant<int, 2>{}, std::integral_constant<int, 64>{});
+  if (bits == 2 && gs == 128) return f(std::integral_constant<int, 2>{}, std::integral_constant<int, 128>{});
+  return nullptr;
+}
+
+int down_passes(int64_t I, int k) { return (int)((I / 32 + 64 / k - 1) / (64 / k)); }
+
+}  // namespace
+
+bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int k, int gs, int bits) {
+  if (T < 1 || T > 8 || H % 32 || I % 32 || H > 4 * 64 * 32) return false;
+  if (!(k == 1 || k == 2 || k == 4 || k == 8 || k == 16)) return false;
+  if (!(bits == 2 || bits == 4) || !(gs == 32 || gs == 64 || gs == 128)) return false;
+  if (H % gs || I % gs) return false;
+  const int P = down_passes(I, k);
+  return P == 1 || P == 2 || P == 3 || P == 4 || P == 6 || P == 8;
+}
+
+int launch_moe_decode(hipStream_t st, const uint16_t* x, const int32_t* idx, const float* wts,
+                      const uint32_t* gw, const uint16_t* gsc, const uint16_t* gbi, const uint32_t* uw,
+                      const uint16_t* usc, const uint16_t* ubi, const uint32_t* dw, const uint16_t* dsc,
+                      const uint16_t* dbi, uint16_t* act, uint16_t* out, int64_t T, int64_t H, int64_t I, int E,
+                      int k, int gs, int bits) {
+  if (!moe_decode_supported(T, H, I, k, gs, bits))
+    return set_error(LISAQ_EUNSUPPORTED, "moe decode: T=%lld H=%lld I=%lld k=%d gs=%d bits=%d", (long long)T,
+                     (long long)H, (long long)I, k, gs, bits);
+  MoeDecodeParams p{x, idx, wts, gw, uw, dw, gsc, gbi, usc, ubi, dsc, dbi, act, out, (int)T, (int)H, (int)I, E, k};
+  const int J = (int)((H / 32 + 63) / 64);
+  const int P = down_passes(I, k);
+  moe_fn gu = by_format(bits, gs, [&](auto B, auto S) { return pick_gu<decltype(B)::value, decltype(S)::value>(J); });
+  moe_fn dc = by_format(bits, gs, [&](auto B, auto S) { return pick_dc<decltype(B)::value, decltype(S)::value>(k, P); });
+  if (!gu || !dc) return set_error(LISAQ_EUNSUPPORTED, "moe decode: no kernel for J=%d P=%d k=%d", J, P, k);
+  hipLaunchKernelGGL(gu, dim3((unsigned)((I + 4 * RPW - 1) / (4 * RPW)), (unsigned)(T * k)), dim3(256), 0, st, p);
+  int rc = check_launch("moe_gate_up_act");
+  if (rc) return rc;
+  hipLaunchKernelGGL(dc, dim3((unsigned)((H + 4 * RPW - 1) / (4 * RPW)), (unsigned)T), dim3(256), 0, st, p);
+  return check_launch("moe_down_combine");
+}
+
+}  // namespace lisaq

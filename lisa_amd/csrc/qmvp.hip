@@ -23,6 +23,7 @@
 // 1, 1/4, 1/16 (powers of two: exact).
 #include "lisaq_common.h"
 #include "qmv.h"
+#include "qmv_dev.h"
 
 #include <cstdlib>
 
@@ -34,79 +35,7 @@
 
 namespace lisaq {
 
-namespace {
-
-typedef __bf16 bf16x2p __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float pdot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2p, a), __builtin_bit_cast(bf16x2p, b), c,
-                                         false);
-}
-
-constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
-constexpr uint32_t kOob = 0x40000000u;  // past every buffer's range; two of them still fit in 32 bits
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
-}
-
-struct PConst {
-  uint32_t magic, m4, m2a, m2b, m2c;
-  __device__ __forceinline__ void init() {
-    magic = 0x43004300u;
-    m4 = 0x000F000Fu;
-    m2a = 0x00030003u;
-    m2b = 0x000C000Cu;
-    m2c = 0x00300030u;
-    // opaque to the optimizer: every (w & mask) | magic selects one v_and_or_b32
-    asm volatile("" : "+v"(magic));
-    asm volatile("" : "+s"(m4), "+s"(m2a), "+s"(m2b), "+s"(m2c));
-  }
-};
-
-// Pairs of one word, each a bf16x2.  4 bits: pair j = (code j, code j+4) as
-// 128+q.  2 bits: pair j = (code j, code j+8) as 128+f*q, f = 1, 4, 16 for
-// j % 3 = 0, 1, 2.
-template <int BITS>
-__device__ __forceinline__ void punpack(uint32_t w, const PConst& k, uint32_t* r) {
-  if constexpr (BITS == 4) {
-    r[0] = (w & k.m4) | k.magic;
-    r[1] = ((w >> 4) & k.m4) | k.magic;
-    r[2] = ((w >> 8) & k.m4) | k.magic;
-    r[3] = ((w >> 12) & k.m4) | k.magic;
-  } else {
-    const uint32_t s1 = w >> 6, s2 = w >> 12;
-    r[0] = (w & k.m2a) | k.magic;
-    r[1] = (w & k.m2b) | k.magic;
-    r[2] = (w & k.m2c) | k.magic;
-    r[3] = (s1 & k.m2a) | k.magic;
-    r[4] = (s1 & k.m2b) | k.magic;
-    r[5] = (s1 & k.m2c) | k.magic;
-    r[6] = (s2 & k.m2a) | k.magic;
-    r[7] = (s2 & k.m2b) | k.magic;
-  }
-}
-
-// Sum over the 64 lanes in a fixed order, all within the VALU (DPP): pair,
-// quad, half-row and row sums, then row_bcast15 / row_bcast31 carry rows
-// 0..2 into lane 63, which holds the total.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __builtin_bit_cast(float,
-                            __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-  v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-  v += dpp_f<0x141, 0xF>(v);  // row_half_mirror
-  v += dpp_f<0x140, 0xF>(v);  // row_mirror: every lane of a row holds the row sum
-  v += dpp_f<0x142, 0xA>(v);  // row_bcast15: rows 1, 3 add the previous row
-  v += dpp_f<0x143, 0xC>(v);  // row_bcast31: rows 2, 3 add lane 31
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-}  // namespace
+using namespace qmvdev;
 
 template <int BITS, int GS, int J, int D, int SBW>
 __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {

@@ -163,3 +163,32 @@ def test_moe_forward_parity(dev, oracle, T):
     assert_close_bf16(from_dev_bf16(out), bf16_bits_to_f32(from_dev_bf16(comb)), what="moe_forward vs step by step")
     assert np.array_equal(from_dev_bf16(comb), oracle.moe_combine(from_dev_bf16(dd), wts.cpu().numpy(), inv, T, k))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T,E,k,H,I,bits,gs", [(1, 128, 8, 2048, 768, 4, 64), (3, 16, 4, 512, 256, 4, 32),
+                                             (8, 32, 2, 1024, 384, 4, 128), (2, 64, 8, 256, 768, 2, 64),
+                                             (5, 32, 16, 128, 1024, 2, 128), (1, 4, 1, 4096, 64, 4, 64)])
+def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
+    """The fused decode path (T <= 8: gate|up+SwiGLU and down+combine kernels)
+    against the generic path (sort, gather_qmm, SwiGLU, combine) on the same
+    inputs: identical routing, outputs within the output tolerance (the two
+    differ only in the order of the matvec sums)."""
+    from lisa_amd import _lib
+
+    rng = np.random.default_rng(T * 1000 + k)
+    stk = lambda n, kk: tuple(a.reshape(E, n, -1) for a in np_linear(rng, E * n, kk, bits, gs))
+    G, U, D = stk(I, H), stk(I, H), stk(H, I)
+    x = np_x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
+    assert _lib.load().lisaq_moe_decode_supported(T, H, I, k, gs, bits) == 1
+    outs = {}
+    for fused in ("1", "0"):
+        monkeypatch.setenv("LISAQ_MOE_FUSED", fused)
+        o, idx, w = ops.moe_forward(to_dev_bf16(x, dev), to_dev(lg, dev), dv[0], dv[1], dv[2], k, gs, bits,
+                                    return_routing=True)
+        outs[fused] = (from_dev_bf16(o), idx.cpu().numpy(), w.cpu().numpy())
+    from lisa_amd.synth import bf16_bits_to_f32
+
+    assert np.array_equal(outs["1"][1], outs["0"][1]) and np.array_equal(outs["1"][2], outs["0"][2])
+    assert_close_bf16(outs["1"][0], bf16_bits_to_f32(outs["0"][0]), what=f"fused vs generic T={T} k={k} bits={bits}")
