@@ -135,9 +135,9 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
 
 // Tile tables of a gather (runs of the sorted ids) into the workspace.
 static int gather_tables(hipStream_t st, const GatherLayout& L, const int32_t* rhs, int64_t R, int64_t N, int E,
-                         void* ws) {
+                         void* ws, const int32_t* offs = nullptr) {
   char* base = (char*)ws;
-  return launch_tile_table(st, rhs, R, E, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN,
+  return launch_tile_table(st, rhs, offs, R, E, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN,
                            (int4*)(base + L.qmv_off), L.qmv_cap, (int4*)(base + L.qmm_off), L.qmm_cap,
                            (int32_t*)base);
 }
@@ -431,7 +431,7 @@ int lisaq_moe_combine(void* stream, const void* down, const float* wts, const in
 
 // MoE forward workspace: [routing ints][x_sorted][gate_out][up_out][down_sorted][gather ws]
 struct MoeLayout {
-  size_t idx, wts, sorted, order, rows, inv, offs, xs, g, u, d, gws, total;
+  size_t idx, wts, sorted, order, rows, inv, offs, hist, xs, g, u, d, gws, total;
 };
 
 static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
@@ -450,6 +450,7 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
   L.rows = take((size_t)R * 4);
   L.inv = take((size_t)R * 4);
   L.offs = take((size_t)(E + 1) * 4);
+  L.hist = take((size_t)sort_hist_ints(R, E) * 4);
   L.xs = take((size_t)R * H * 2);
   L.g = take((size_t)R * I * 2);
   L.u = take((size_t)R * I * 2);
@@ -507,7 +508,9 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
                              (const uint16_t*)usc, (const uint16_t*)ubi, dw, (const uint16_t*)dsc,
                              (const uint16_t*)dbi, g, (uint16_t*)out, T, H, I, E, k, gs, bits);
   }
-  if ((rc = lisaq_moe_sort(st, idx, R, E, k, sorted, order, rows, inv, offs))) return rc;
+  LISAQ_REQUIRE(E <= 1024, LISAQ_EINVAL_SHAPE, "moe_forward: need E <= 1024 (E=%d)", E);
+  if ((rc = launch_sort_parallel(st, idx, R, E, k, sorted, order, rows, inv, offs, (int32_t*)(B + L.hist))))
+    return rc;
   if ((rc = lisaq_gather_rows(st, x, rows, xs, R, H))) return rc;
   // gate and up share one set of tile tables; every run is at most T rows
   if ((rc = validate_mm("moe_forward gate", xs, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
@@ -518,11 +521,11 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   LISAQ_REQUIRE(GU.total <= gws_bytes && DN.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
   if ((GU.qmm_cap > 0 || DN.qmm_cap > 0) && (H % 64 || I % 64))
     return set_error(LISAQ_EUNSUPPORTED, "moe_forward: H, I must be multiples of 64 for the matmul path");
-  if ((rc = gather_tables(st, GU, sorted, R, I, E, gws))) return rc;
+  if ((rc = gather_tables(st, GU, sorted, R, I, E, gws, offs))) return rc;
   if ((rc = gather_launch(st, GU, xs, gw, gsc, gbi, g, R, I, H, gs, bits, gws))) return rc;
   if ((rc = gather_launch(st, GU, xs, uw, usc, ubi, u, R, I, H, gs, bits, gws))) return rc;
   if ((rc = lisaq_swiglu(st, g, u, g, R * I))) return rc;
-  if ((rc = gather_tables(st, DN, sorted, R, H, E, gws))) return rc;
+  if ((rc = gather_tables(st, DN, sorted, R, H, E, gws, offs))) return rc;
   if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;
   return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
 }

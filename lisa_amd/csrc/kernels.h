@@ -25,7 +25,14 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const int32_t* idx, con
                       const uint16_t* dbi, uint16_t* act, uint16_t* out, int64_t T, int64_t H, int64_t I, int E,
                       int k, int gs, int bits);
 constexpr int kTileTableMaxExperts = 16384;
-int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int E, int N, int limit, int VR, int BM, int BN,
-                      int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap, int32_t* counts);
+// gather tile tables from the sorted ids (offs == nullptr) or from the sort's
+// expert offsets [E+1]
+int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E, int N, int limit,
+                      int VR, int BM, int BN, int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap,
+                      int32_t* counts);
+// stable counting sort over many workgroups; hist: sort_hist_ints(R, E) ints of workspace
+int sort_hist_ints(int64_t R, int E);
+int launch_sort_parallel(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,
+                         int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets, int32_t* hist);
 
 }  // namespace lisaq

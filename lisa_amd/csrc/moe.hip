@@ -197,6 +197,155 @@ int launch_sort(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k,
 }
 
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// The same stable counting sort over many workgroups (the MoE forward path,
+// which has a workspace): blocks of kSortChunk ids.  Pass 1 counts each
+// block's ids per expert (row E counts invalid ids); pass 2 turns the counts
+// into each block's first position per expert (expert offset + the block's
+// predecessors' counts) and writes the expert offsets (offsets[E] = -1 on
+// invalid ids); pass 3 places each block's ids in input order, exactly as the
+// one-workgroup sort places a chunk.  All loads of a block are issued
+// together.
+constexpr int kSortChunk = 2048;
+constexpr int kSortPer = kSortChunk / 256;  // ids per thread
+
+__global__ __launch_bounds__(256) void sort_count_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
+                                                         int32_t* __restrict__ hist, int B) {
+  extern __shared__ int32_t cnt[];  // [E + 1]
+  const int b = blockIdx.x, tid = threadIdx.x;
+  for (int e = tid; e <= E; e += 256) cnt[e] = 0;
+  const int64_t i0 = (int64_t)b * kSortChunk;
+  int v[kSortPer];
+#pragma unroll
+  for (int j = 0; j < kSortPer; ++j) {
+    const int64_t i = i0 + j * 256 + tid;
+    v[j] = i < R ? ids[i] : -2;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kSortPer; ++j) {
+    if (v[j] == -2) continue;
+    atomicAdd(&cnt[(v[j] >= 0 && v[j] < E) ? v[j] : E], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += 256) hist[(int64_t)e * B + b] = cnt[e];
+}
+
+__global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ hist, int B, int E, int64_t R,
+                                                         int32_t* __restrict__ offsets) {
+  __shared__ int wsum[16], s_bad;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // per expert: exclusive prefix over the blocks (16 loads in flight at a time)
+  int total = 0;
+  if (tid == 0) {  // invalid ids (row E)
+    int nb = 0;
+    for (int b = 0; b < B; ++b) nb += hist[(int64_t)E * B + b];
+    s_bad = nb;
+  }
+  if (tid < E) {
+    int32_t* row = hist + (int64_t)tid * B;
+    for (int b0 = 0; b0 < B; b0 += 16) {
+      int c[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) c[u] = b0 + u < B ? row[b0 + u] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (b0 + u < B) {
+          row[b0 + u] = total;
+          total += c[u];
+        }
+    }
+  }
+  // exclusive scan of the expert totals (E <= 1024: one per thread)
+  const int mine = tid < E ? total : 0;
+  int inc = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int a = __shfl_up(inc, d);
+    if (lane >= d) inc += a;
+  }
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int w2 = 0; w2 < wv; ++w2) base += wsum[w2];
+  const int off = base + inc - mine;
+  if (tid < E) {
+    int32_t* row = hist + (int64_t)tid * B;
+    for (int b = 0; b < B; ++b) row[b] += off;
+    offsets[tid] = off;
+  }
+  if (tid == 0) offsets[E] = s_bad ? -1 : (int32_t)R;
+}
+
+__global__ __launch_bounds__(256) void sort_scatter_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
+                                                           int top_k, const int32_t* __restrict__ base,
+                                                           int B, const int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ sorted_idx,
+                                                           int32_t* __restrict__ order,
+                                                           int32_t* __restrict__ token_rows,
+                                                           int32_t* __restrict__ inverse) {
+  extern __shared__ int32_t sm2[];
+  int32_t* running = sm2;     // [E]
+  int32_t* wcnt = sm2 + E;    // [4][E]
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (offsets[E] < 0) return;  // invalid ids: nothing is placed
+  const int64_t i0 = (int64_t)b * kSortChunk;
+  int v[kSortPer];
+#pragma unroll
+  for (int j = 0; j < kSortPer; ++j) {
+    const int64_t i = i0 + j * 256 + tid;
+    v[j] = i < R ? ids[i] : -1;
+  }
+  for (int e = tid; e < E; e += 256) running[e] = base[(int64_t)e * B + b];
+  for (int e = tid; e < 4 * E; e += 256) wcnt[e] = 0;
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  __syncthreads();
+#pragma unroll 1
+  for (int j = 0; j < kSortPer; ++j) {
+    const int64_t i = i0 + j * 256 + tid;
+    const bool valid = i < R;
+    const int e = v[j];
+    uint64_t peers = __ballot(valid);
+    for (int bb = 0; bb < nbits; ++bb) {
+      const uint64_t ones = __ballot(valid && ((e >> bb) & 1));
+      peers &= ((e >> bb) & 1) ? ones : ~ones;
+    }
+    const uint64_t lower = peers & ((1ull << lane) - 1ull);
+    const int rank = __popcll(lower);
+    const bool leader = valid && lower == 0;
+    if (leader) wcnt[wave * E + e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int pos = running[e] + rank;
+      for (int w2 = 0; w2 < wave; ++w2) pos += wcnt[w2 * E + e];
+      sorted_idx[pos] = e;
+      order[pos] = (int32_t)i;
+      token_rows[pos] = (int32_t)(i / top_k);
+      inverse[i] = pos;
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&running[e], __popcll(peers));
+      wcnt[wave * E + e] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+int sort_hist_ints(int64_t R, int E) { return (int)((E + 1) * ((R + kSortChunk - 1) / kSortChunk)); }
+
+int launch_sort_parallel(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,
+                         int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets, int32_t* hist) {
+  if (R == 0) return LISAQ_OK;
+  const int B = (int)((R + kSortChunk - 1) / kSortChunk);
+  hipLaunchKernelGGL(sort_count_kernel, dim3(B), dim3(256), sizeof(int32_t) * (E + 1), st, ids, R, E, hist, B);
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, st, hist, B, E, R, offsets);
+  hipLaunchKernelGGL(sort_scatter_kernel, dim3(B), dim3(256), sizeof(int32_t) * 5 * E, st, ids, R, E, top_k, hist,
+                     B, offsets, sorted_idx, order, token_rows, inverse);
+  return check_launch("moe_sort_parallel");
+}
+
 __global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __restrict__ x,
                                                           const int32_t* __restrict__ rows,
                                                           uint16_t* __restrict__ out, int64_t R,
@@ -360,8 +509,9 @@ int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const i
 //     (ids out of [0, E) or not sorted: no tiles at all, counts[2] = 1);
 //  2. per-expert tile counts and an exclusive scan over the experts;
 //  3. each thread writes the tiles of its experts, then the padding.
-__global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restrict__ ids, int64_t R, int E, int N,
-                                                          int limit, int VR, int BM, int BN,
+__global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restrict__ ids,
+                                                          const int32_t* __restrict__ offs, int64_t R, int E,
+                                                          int N, int limit, int VR, int BM, int BN,
                                                           int4* __restrict__ qmv_tab, int qmv_cap,
                                                           int4* __restrict__ qmm_tab, int qmm_cap,
                                                           int32_t* __restrict__ counts) {
@@ -373,16 +523,37 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   for (int e = tid; e < E; e += 1024) rstart[e] = rend[e] = 0;
   if (tid == 0) s_bad = 0;
   __syncthreads();
-  for (int64_t i = tid; i < R; i += 1024) {
-    const int id = ids[i];
-    const int prev = i > 0 ? ids[i - 1] : -1;
-    const int next = i + 1 < R ? ids[i + 1] : E;
-    if (id < 0 || id >= E || prev > id) {
-      s_bad = 1;  // (every writer stores the same value)
-      continue;
+  if (offs) {
+    // runs straight from the sort's expert offsets (offs[E] < 0: bad ids)
+    if (offs[E] < 0) s_bad = 1;
+    for (int e = tid; e < E; e += 1024) {
+      rstart[e] = offs[e];
+      rend[e] = offs[e + 1];
     }
-    if (prev != id) rstart[id] = (int)i;
-    if (next != id) rend[id] = (int)(i + 1);
+  } else {
+    // runs of the sorted ids; 8 ids per thread per batch, loads issued together
+    constexpr int U = 8;
+    for (int64_t i0 = 0; i0 < R; i0 += 1024 * U) {
+      int id[U], prev[U], next[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + u * 1024 + tid;
+        id[u] = i < R ? ids[i] : 0;
+        prev[u] = (i > 0 && i < R) ? ids[i - 1] : -1;
+        next[u] = i + 1 < R ? ids[i + 1] : E;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + u * 1024 + tid;
+        if (i >= R) continue;
+        if (id[u] < 0 || id[u] >= E || prev[u] > id[u]) {
+          s_bad = 1;  // (every writer stores the same value)
+          continue;
+        }
+        if (prev[u] != id[u]) rstart[id[u]] = (int)i;
+        if (next[u] != id[u]) rend[id[u]] = (int)(i + 1);
+      }
+    }
   }
   __syncthreads();
   const int nt32 = (N + VR - 1) / VR;  // matvec tiles per run
@@ -449,8 +620,9 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   for (int t = tot_m + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
 }
 
-int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int E, int N, int limit, int VR, int BM, int BN,
-                      int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap, int32_t* counts) {
+int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E, int N, int limit,
+                      int VR, int BM, int BN, int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap,
+                      int32_t* counts) {
   if (E > kTileTableMaxExperts)
     return set_error(LISAQ_EUNSUPPORTED, "gather_qmm: E=%d experts (at most %d)", E, kTileTableMaxExperts);
   const int lds = 2 * E * 4;
@@ -458,8 +630,8 @@ int launch_tile_table(hipStream_t st, const int32_t* ids, int64_t R, int E, int 
     hipError_t e = hipFuncSetAttribute((const void*)tile_table_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return set_error(LISAQ_EHIP, "gather_tile_table: LDS %d bytes: %s", lds, hipGetErrorString(e));
   }
-  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), lds, st, ids, R, E, N, limit, VR, BM, BN, qmv_tab,
-                     qmv_cap, qmm_tab, qmm_cap, counts);
+  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), lds, st, ids, offs, R, E, N, limit, VR, BM, BN,
+                     qmv_tab, qmv_cap, qmm_tab, qmm_cap, counts);
   return check_launch("gather_tile_table");
 }
 

@@ -192,3 +192,30 @@ def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
 
     assert np.array_equal(outs["1"][1], outs["0"][1]) and np.array_equal(outs["1"][2], outs["0"][2])
     assert_close_bf16(outs["1"][0], bf16_bits_to_f32(outs["0"][0]), what=f"fused vs generic T={T} k={k} bits={bits}")
+
+
+def test_moe_forward_generic_equals_composition(dev, monkeypatch):
+    """moe_forward's generic path (multi-workgroup counting sort, tile tables
+    built from the expert offsets) against the same steps composed from the
+    public entry points (one-workgroup sort, tile tables from the sorted ids):
+    bit-identical, at a size where the sort spans several workgroups
+    (T=600, k=8: 4800 ids)."""
+    import torch
+
+    monkeypatch.setenv("LISAQ_MOE_FUSED", "0")
+    rng = np.random.default_rng(600)
+    T, E, k, H, I = 600, 64, 8, 128, 64
+    G, U, D = _expert_stack(rng, E, I, H), _expert_stack(rng, E, I, H), _expert_stack(rng, E, H, I)
+    x = to_dev_bf16(np_x(rng, T, H), dev)
+    lg = to_dev(rng.standard_normal((T, E)).astype(np.float32), dev)
+    dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
+    out, idx, wts = ops.moe_forward(x, lg, dv[0], dv[1], dv[2], k, return_routing=True)
+    ridx, rw = ops.moe_route(lg, k)
+    assert torch.equal(ridx, idx) and torch.equal(rw, wts)
+    srt, order, rows, inv, offs = ops.moe_sort(ridx.reshape(-1), E, k)
+    xs = ops.gather_rows(x, rows)
+    g = ops.gather_qmm(xs, *dv[0], rhs_indices=srt)
+    u = ops.gather_qmm(xs, *dv[1], rhs_indices=srt)
+    d = ops.gather_qmm(ops.swiglu(g, u), *dv[2], rhs_indices=srt)
+    ref = ops.moe_combine(d, rw.reshape(-1), inv, T, k)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
