@@ -35,7 +35,7 @@ METRIC = "4-bit qmv GB/s (% HBM peak) @M=1; qmm TFLOP/s (% bf16 MFMA peak) @M=20
 # scaled by the counter's reading for a 64 MiB device copy (see the profiles/ summaries for the
 # commands and raw counts).
 QMV_TRAFFIC_BYTES = round((24566.0 * 1.9993 + 136.0) * 1024)
-QMM_TRAFFIC_BYTES = round((251777.7 * 1.9993 + 69632.0) * 1024)
+QMM_TRAFFIC_BYTES = round((253450.3 * 1.9993 + 70333.7) * 1024)
 QMV_KERNEL = "lisaq::qmvp_kernel<4, 64, 3, 2, 16>"
 QMM_KERNEL = "lisaq::qmm_kernel<4, 64, 6, 1, 8, false>"  # M=2048: 192-row tiles, eight waves
 
