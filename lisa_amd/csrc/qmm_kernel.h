@@ -1,0 +1,525 @@
+// Prefill matmul (qmm) for MLX affine-quantized weights on gfx950.
+//
+// Replaces the Metal kernel affine_qmm_t (crates/lisa-mlx/src/shaders/common/
+// matmul/quantized.metal:1208-1326 with QuantizedBlockLoader :585-703).
+// Arithmetic contract (same as the reference loader): every weight is
+// dequantized to the compute type, w = bf16(scale*q + bias) with scale/bias
+// in f32 (quantized.metal:497-498, 528-533), then y = x . w^T with an f32
+// accumulator (steel BlockMMA, gemm.metal:905-919), one bf16 rounding.
+//
+// MI355X design:
+//  * Workgroup = 4 waves side by side along N.  The x tile (BM rows x 64 K)
+//    is staged through LDS (double-buffered) and shared by the 4 waves; each
+//    wave streams and dequantizes only its own W rows, straight from global
+//    memory into the bf16 B operands of v_mfma_f32_32x32x16_bf16 (no LDS round
+//    trip for W, no duplicated dequant work).
+//  * Per lane and K-step of 64: one 16-byte load of packed codes (4-bit), 8
+//    codes per u32 split with one mask into bytes, v_cvt_f32_ubyte*, one FMA
+//    with the group's scale/bias, v_cvt_pk_bf16_f32.
+//  * The next K-step's x tile and W words are fetched while the current one
+//    runs on the matrix cores.
+#pragma once
+#include "lisaq_common.h"
+#include "qmm.h"
+#include <type_traits>
+#include <utility>
+
+namespace lisaq {
+
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Byte I of a word as f32: one v_cvt_f32_ubyte<I>.
+template <int I>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  return (float)((v >> (8 * I)) & 0xFFu);
+}
+// A word of masked codes made opaque to the optimizer, which would otherwise
+// fold the mask into each byte extraction (v_bfe + v_cvt_f32_ubyte0 instead
+// of one v_cvt_f32_ubyte<I>).
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Dequantize the 8 codes of one u32 (4-bit) into 4 bf16x2 in natural K order.
+__device__ __forceinline__ void deq4(uint32_t w, float s, float b, uint32_t* o) {
+  const uint32_t lo = opaque(w & 0x0F0F0F0Fu);         // codes 0,2,4,6
+  const uint32_t hi = opaque((w >> 4) & 0x0F0F0F0Fu);  // codes 1,3,5,7
+  o[0] = pk_bf16(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
+  o[1] = pk_bf16(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
+  o[2] = pk_bf16(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
+  o[3] = pk_bf16(fmaf(s, ubyte_f32<3>(lo), b), fmaf(s, ubyte_f32<3>(hi), b));
+}
+
+// Dequantize the 16 codes of one u32 (2-bit) into 8 bf16x2 in natural K order.
+__device__ __forceinline__ void deq2(uint32_t w, float s, float b, uint32_t* o) {
+  const uint32_t c0 = opaque(w & 0x03030303u);         // codes 0,4,8,12
+  const uint32_t c1 = opaque((w >> 2) & 0x03030303u);  // codes 1,5,9,13
+  const uint32_t c2 = opaque((w >> 4) & 0x03030303u);  // codes 2,6,10,14
+  const uint32_t c3 = opaque((w >> 6) & 0x03030303u);  // codes 3,7,11,15
+  o[0] = pk_bf16(fmaf(s, ubyte_f32<0>(c0), b), fmaf(s, ubyte_f32<0>(c1), b));
+  o[1] = pk_bf16(fmaf(s, ubyte_f32<0>(c2), b), fmaf(s, ubyte_f32<0>(c3), b));
+  o[2] = pk_bf16(fmaf(s, ubyte_f32<1>(c0), b), fmaf(s, ubyte_f32<1>(c1), b));
+  o[3] = pk_bf16(fmaf(s, ubyte_f32<1>(c2), b), fmaf(s, ubyte_f32<1>(c3), b));
+  o[4] = pk_bf16(fmaf(s, ubyte_f32<2>(c0), b), fmaf(s, ubyte_f32<2>(c1), b));
+  o[5] = pk_bf16(fmaf(s, ubyte_f32<2>(c2), b), fmaf(s, ubyte_f32<2>(c3), b));
+  o[6] = pk_bf16(fmaf(s, ubyte_f32<3>(c0), b), fmaf(s, ubyte_f32<3>(c1), b));
+  o[7] = pk_bf16(fmaf(s, ubyte_f32<3>(c2), b), fmaf(s, ubyte_f32<3>(c3), b));
+}
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N-1>{})
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int BITS>
+struct MGeo {
+  static constexpr int PACK = 32 / BITS;
+  static constexpr int WPL = 32 / PACK;  // words per lane per K-step (32 codes)
+};
+
+constexpr int BK = 64;
+// x tile in LDS: rows of 64 bf16 (128 B) written by direct-to-LDS loads, one
+// wave instruction = 8 rows = 1 KB.  The 16-byte chunks of a row are XOR-
+// swizzled by (row % 8) ^ (row / 8 % 2): an A-operand read (lanes 0-31 on
+// rows 0-31, one logical chunk) then puts any 8 consecutive lanes on 8
+// distinct 16-byte bank groups of a 128-byte line and any 16 consecutive lanes
+// on 16 distinct ones of a 256-byte line, i.e. no bank conflicts whether the
+// LDS serves 8 or 16 lanes of a 128-bit read per clock.
+constexpr int XG = 1024;  // bytes per 8-row group
+constexpr int NBUF = 3;   // LDS ring: step k+2 lands while step k runs
+
+__device__ __forceinline__ int x_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int x_lds_off(int row, int chunk) { return row * 128 + ((chunk ^ x_swz(row)) << 4); }
+// Packed W tile (4-bit: 32 bytes = two 16-byte halves per row and K-step):
+// the halves of a row swap when bit 2 ^ bit 3 of the row is set, so the
+// B-operand reads (lanes on 32 consecutive rows, one half) are conflict-free
+// in the same sense.
+__device__ __forceinline__ int w_swz(int row) { return ((row >> 2) ^ (row >> 3)) & 1; }
+
+// 16 / 4 / 2 bytes per lane from global memory straight into LDS (lane l
+// writes lds + size*l; lds must be wave-uniform).
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+__device__ __forceinline__ void load_lds2(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 2, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (expcnt, lgkmcnt left alone): the direct-to-LDS loads
+// are not tracked by the compiler's own waits.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// s_waitcnt lgkmcnt(0) (vmcnt, expcnt left alone)
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier without the memory fence of __syncthreads(): the fence
+// would wait for every outstanding global load, including the direct-to-LDS
+// copies just issued for later steps; the waits above say exactly which
+// copies must have landed.  The scheduling barriers keep LDS reads on their
+// side of it.
+__device__ __forceinline__ void block_sync() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BITS, int GS, int MT, int NT, int WN>
+struct QmmLds {
+  static constexpr int BM = 32 * MT, BN = WN * 32 * NT;
+  static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
+  static constexpr int X = BM / 8 * XG;            // x tile
+  static constexpr int W = BN * RB;                // packed W tile
+  static constexpr int S = BN * 4;                 // scales: the aligned bf16 pair holding the step's group(s)
+  static constexpr int WSTAGE = W + 2 * S;         // packed W + scales + biases of one step
+  static constexpr int W0 = NBUF * X;              // W ring after the x ring
+  static constexpr int TOTAL = NBUF * (X + WSTAGE);
+};
+
+// WN waves side by side along N, each all BM rows x 32*NT columns: four
+// waves (one per SIMD, NT = 2, 256 accumulator registers) or eight (two per
+// SIMD, NT = 1, 128 accumulator registers: a SIMD's second wave fills the
+// matrix-core bubbles of the first).  Either way every W element is
+// dequantized once per workgroup.
+template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT>
+__global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
+  using G = MGeo<BITS>;
+  using L = QmmLds<BITS, GS, MT, NT, WN>;
+  constexpr int BM = L::BM;
+  constexpr int BN = L::BN;
+  constexpr int NWV = WN;  // waves per workgroup
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int wn = wave;  // column group
+  const int col = lane & 31;
+  const int h = lane >> 5;
+
+  const uint32_t* w = p.w;
+  const uint16_t* sc = p.s;
+  const uint16_t* bi = p.b;
+  const uint16_t* x = p.x;
+  uint16_t* y = p.y;
+  int M = p.M;
+  int m0, nt0, split = 0;
+  if (p.tiles) {
+    const int4 t = p.tiles[blockIdx.x];
+    if (t.x < 0) return;
+    const int64_t e = t.x;
+    w += e * (int64_t)p.N * (p.K / G::PACK);
+    sc += e * (int64_t)p.N * p.G;
+    bi += e * (int64_t)p.N * p.G;
+    x += (int64_t)t.y * p.K;
+    y += (int64_t)t.y * p.N;
+    M = t.z;
+    m0 = 0;
+    nt0 = t.w * BN;
+  } else {
+    // row-block major: consecutive workgroups share an x row block and walk W;
+    // with a split over K, split s of every tile comes after split s-1's
+    const int gn = (p.N + BN - 1) / BN, T = gn * ((M + BM - 1) / BM);
+    const int tile = blockIdx.x % T;
+    split = blockIdx.x / T;
+    nt0 = (tile % gn) * BN;
+    m0 = (tile / gn) * BM;
+  }
+
+  // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
+  // matrix are clamped to the last one, their results are never stored)
+  // x: BM/8 instructions of 1 KB, XI per wave; lane l fills row 8g + l/8,
+  // physical chunk l%8 (= logical chunk (l%8) ^ x_swz(row), and x_swz(row) =
+  // l/8 ^ (g % 2))
+  constexpr int XI = BM / 8 / NWV;
+  // element offsets, recomputed per copy to save registers (the host checks
+  // that x fits 2^31 elements)
+  const int xrow0 = m0 + wave * XI * 8 + (lane >> 3);
+  const uint32_t xchunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 3);
+  auto xoff = [&](int i) -> uint32_t {
+    const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
+    return (uint32_t)row * (uint32_t)p.K + (xchunk ^ (((wave * XI + i) & 1) << 3));
+  };
+  // W: BN rows x RB bytes, row-major; 16 bytes per lane: WB bytes per wave in
+  // WI instructions (the last lanes idle when a wave's share is under 1 KB)
+  constexpr int WB = L::W / NWV;                  // bytes per wave
+  constexpr int WI = WB >= 1024 ? WB / 1024 : 1;  // instructions per wave
+  constexpr int WLANES = WB >= 1024 ? 64 : WB / 16;
+  static_assert(L::W % NWV == 0 && (WB >= 1024 ? WB % 1024 == 0 : WB % 16 == 0), "W tile geometry");
+  const unsigned char* wsrc[WI];
+  const int64_t rowbytes = (int64_t)p.K * BITS / 8;
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int off = wave * WB + i * 1024 + lane * 16;  // byte in the W tile
+    int n = nt0 + off / L::RB;
+    n = n < p.N ? n : p.N - 1;
+    // 4-bit: physical half (off / 16) % 2 of tile row off / 32 holds logical
+    // half ^ w_swz(row)
+    const int lb = BITS == 4 ? (off % L::RB) ^ (w_swz(off / L::RB) << 4) : off % L::RB;
+    wsrc[i] = reinterpret_cast<const unsigned char*>(w) + n * rowbytes + lb;
+  }
+  // scales / biases: per row the 4-byte-aligned bf16 pair holding the step's
+  // group(s); 64 rows per instruction (BN/64 instructions per array, spread
+  // over the waves)
+  constexpr int SI = BN / 64;                  // instructions per array
+  constexpr int SBI = SI * 2 / NWV;            // scale/bias instructions per wave
+  static_assert(SBI >= 1 && SI * 2 % NWV == 0, "scale tile geometry");
+  constexpr int VM_X = XI, VM_W = WI + SBI;    // DMA instructions per wave: x tile, W stage
+  // copies i0 <= i < i1 of the x tile (i0, i1 compile-time after inlining)
+  auto issue_x = [&](int k, int stage, int i0, int i1) {
+    unsigned char* st = smem + stage * L::X;
+    const int k0 = k * BK;
+#pragma unroll
+    for (int i = 0; i < XI; ++i)
+      if (i >= i0 && i < i1) load_lds16(x + xoff(i) + k0, st + (wave * XI + i) * XG);
+  };
+  // copy q of the W stage of step k: q < WI packed W, else scale/bias copy q - WI
+  auto issue_w_part = [&](int k, int stage, int q) {
+    unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
+    const int k0 = k * BK;
+    if (q < WI) {
+      if (WLANES == 64 || lane < WLANES) load_lds16(wsrc[q] + (int64_t)k0 * BITS / 8, st + wave * WB + q * 1024);
+      return;
+    }
+    const int g = k0 / GS;
+    const int idx = wave + NWV * (q - WI);  // 0 .. 2*SI-1: s row blocks, then b row blocks
+    const bool is_b = idx >= SI;
+    const int blk = is_b ? idx - SI : idx;
+    // (lanes of this instruction load rows blk*64 + lane)
+    const int64_t roff = (int64_t)(nt0 + blk * 64 + lane < p.N ? nt0 + blk * 64 + lane : p.N - 1) * p.G + g;
+    const uint16_t* src = (is_b ? bi : sc) + (roff & ~(int64_t)1);  // (G is even: 4-byte aligned)
+    load_lds4(src, st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
+  };
+  auto issue_w = [&](int k, int stage) {
+#pragma unroll
+    for (int q = 0; q < WI + SBI; ++q) issue_w_part(k, stage, q);
+  };
+
+  // ---- one K-step's W of this lane (LDS stage): packed words, scale, bias
+  typedef typename std::conditional<G::WPL == 4, u32x4, u32x2>::type WV;
+  struct WLane {
+    WV w[NT];
+    uint16_t s[NT], b[NT];  // raw bf16 bits (converted where used)
+  };
+  auto read_w = [&](int k, int stage, WLane& o) {
+    const unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
+    const int g0 = k * BK / GS;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int r = (wn * NT + nt) * 32 + col;
+      // half of the staged pair: the lane's group (gs 32: the step's two
+      // groups, pair-aligned since G is even; else the element's parity)
+      const int n = nt0 + r < p.N ? nt0 + r : p.N - 1;
+      const int half = GS == 32 ? h : (int)(((int64_t)n * p.G + g0) & 1);
+      const int si = r * 4 + half * 2;
+      o.s[nt] = *reinterpret_cast<const uint16_t*>(st + L::W + si);
+      o.b[nt] = *reinterpret_cast<const uint16_t*>(st + L::W + L::S + si);
+      const int hp = BITS == 4 ? h ^ w_swz(r) : h;
+      o.w[nt] = *reinterpret_cast<const WV*>(st + r * L::RB + hp * (4 * G::WPL));
+    }
+  };
+  // s, b as f32 for one column tile of a W lane
+  auto sf = [&](const WLane& r, int nt) { return bf2f(r.s[nt]); };
+  auto bf = [&](const WLane& r, int nt) { return bf2f(r.b[nt]); };
+  // dequantize all words of a W lane into B operands [nt][16] bf16x2
+  auto dequant_all = [&](const WLane& r, uint32_t (*bop)[16]) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int jw = 0; jw < G::WPL; ++jw) {
+        if (BITS == 4) deq4(r.w[nt][jw], sf(r, nt), bf(r, nt), &bop[nt][jw * 4]);
+        else deq2(r.w[nt][jw], sf(r, nt), bf(r, nt), &bop[nt][jw * 8]);
+      }
+  };
+
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x16{};
+
+  // Pipeline.  Step k reads x stage k % 3 and its B operands (dequantized
+  // during step k-1), dequantizes step k+1's W (W stage (k+1) % 3, read from
+  // LDS one step earlier) into the other B buffer, and copies x(k+2) and
+  // W(k+3) into the stages freed by step k-1.  Copies past the last step
+  // re-read it, so every step issues the same number of copies and the waits
+  // are constants.
+  // K-steps of this workgroup: [kb, kb + nk) (the whole K unless split)
+  const int nk_all = p.K / BK;
+  const int per = (nk_all + p.ksplit - 1) / p.ksplit;
+  const int kb = split * per;
+  const int nk = nk_all - kb < per ? nk_all - kb : per;  // (host: every split has >= 1 step)
+  auto kc = [&](int k) { return kb + (k < nk ? k : nk - 1); };
+  uint32_t bA[NT][16], bB[NT][16];  // B operands of the current / next step
+  issue_x(kc(0), 0, 0, XI);
+  issue_w(kc(0), 0);
+  issue_w(kc(1), 1);
+  issue_x(kc(1), 1, 0, XI);
+  issue_w(kc(2), 2);
+  wait_vm<VM_X + VM_W>();  // x(0), W(0), W(1) landed (this wave's part)
+  block_sync();
+  {
+    WLane w0;
+    read_w(kc(0), 0, w0);
+    dequant_all(w0, bA);
+  }
+  auto read_a1 = [&](const unsigned char* xb, int j, int mt) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(xb + x_lds_off(mt * 32 + col, 4 * h + j));
+  };
+  u32x4 a0[MT], a1[MT];
+  WLane wA, wB;  // W of the step after the current one (alternating)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) a0[mt] = read_a1(smem, 0, mt);
+  read_w(kc(1), 1, wA);
+
+  // One step as 4 * MT * NT slots, each one matrix instruction plus its share
+  // of the other work, in program order (scheduling barriers between slots):
+  //  * sub-step j's first MT slots read the A operands of sub-step j+1
+  //    (sub-step 3: of the next step's sub-step 0, after the barrier);
+  //  * the step's copies are spread evenly over sub-steps 0-2, so the texture
+  //    path drains each before the next arrives and the wave never stalls
+  //    issuing one;
+  //  * the dequantization of the next step's W is cut into pieces of one
+  //    bf16 pair (about five VALU ops) spread evenly over all slots, so the
+  //    VALU work hides under the matrix instructions;
+  //  * between sub-steps 2 and 3: wait for x(k+1), W(k+2) and for this
+  //    step's LDS reads, then the workgroup barrier.
+  constexpr int NMF = MT * NT;
+  constexpr int SLOTS = 4 * NMF;
+  constexpr int NCOPY = XI + WI + SBI;               // copies per wave and step
+  constexpr int PPW = BITS == 4 ? 4 : 8;             // dequant pieces per packed word
+  constexpr int NPIECE = NT * G::WPL * PPW;          // dequant pieces per step
+  static_assert(NCOPY <= 3 * NMF && NPIECE <= SLOTS, "slot plan");
+  int xs = 0, ws1 = 1;  // x stage of step k, W stage of step k+1
+  auto step = [&](int kt, uint32_t (*bcur)[16], uint32_t (*bnxt)[16], const WLane& wn, WLane& wnn) {
+    const int xs2 = xs == 0 ? 2 : xs - 1;    // (k+2) % 3
+    const int ws3 = ws1 == 0 ? 2 : ws1 - 1;  // (k+3) % 3 = k % 3
+    const int xs1 = xs == 2 ? 0 : xs + 1;    // (k+1) % 3
+    const int ws2 = ws1 == 2 ? 0 : ws1 + 1;  // (k+2) % 3
+    const unsigned char* xb = smem + xs * L::X;
+    const unsigned char* xb1 = smem + xs1 * L::X;
+    uint32_t lo[NT][G::WPL], hi[NT][G::WPL], c4[NT][G::WPL][4];  // split codes of the words being dequantized
+    static_for<SLOTS>([&](auto SI) {
+      constexpr int sl = decltype(SI)::value;
+      constexpr int j = sl / NMF, i = sl % NMF;
+      constexpr int nt = i / MT, mt = i % MT;
+      if constexpr (i == 0 && j == 3) {
+        wait_lgkm0();
+        wait_vm<VM_X + VM_W>();
+        block_sync();
+      }
+      // matrix instruction (issued before the slot's LDS reads, so its operand
+      // wait does not also wait for them)
+      {
+        const u32x4 aw = (j & 1) ? a1[mt] : a0[mt];
+        const u32x4 bw = u32x4{bcur[nt][4 * j], bcur[nt][4 * j + 1], bcur[nt][4 * j + 2], bcur[nt][4 * j + 3]};
+        // W as the row operand, x as the column operand: the accumulator is
+        // y^T, so a lane holds runs of 4 consecutive outputs of one row
+        acc[mt][nt] = mfma32x32x16(as_bf16x8(bw), as_bf16x8(aw), acc[mt][nt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // the W words of the step after next, first thing after the barrier (the
+      // next step's first dequantization piece needs them)
+      if constexpr (j == 3 && i == 0) read_w(kc(kt + 2), ws2, wnn);
+      // A operands of the next sub-step, two per slot in the sub-step's first
+      // slots: they have landed by the sub-step's end (where the compiler
+      // waits for all outstanding LDS reads)
+      static_for<2>([&](auto RI) {
+        constexpr int r = 2 * i + decltype(RI)::value;
+        if constexpr (r < MT) {
+          if constexpr (j == 0) a1[r] = read_a1(xb, 1, r);
+          if constexpr (j == 1) a0[r] = read_a1(xb, 2, r);
+          if constexpr (j == 2) a1[r] = read_a1(xb, 3, r);
+          if constexpr (j == 3) a0[r] = read_a1(xb1, 0, r);
+        }
+      });
+
+      // copies: copy q at slot q * (3 NMF) / NCOPY
+      static_for<NCOPY>([&](auto QI) {
+        constexpr int q = decltype(QI)::value;
+        if constexpr (q * 3 * NMF / NCOPY == sl) {
+          if constexpr (q < XI) issue_x(kc(kt + 2), xs2, q, q + 1);
+          else issue_w_part(kc(kt + 3), ws3, q - XI);
+        }
+      });
+      // dequant pieces: piece d at slot d * SLOTS / NPIECE
+      static_for<NPIECE>([&](auto DI) {
+        constexpr int d = decltype(DI)::value;
+        if constexpr (d * SLOTS / NPIECE == sl) {
+          constexpr int dnt = d / (G::WPL * PPW), dw = d / PPW % G::WPL, dp = d % PPW;
+          const uint32_t wv = wn.w[dnt][dw];
+          const float s_ = sf(wn, dnt), b_ = bf(wn, dnt);
+          if constexpr (BITS == 4) {
+            if constexpr (dp == 0) {
+              lo[dnt][dw] = opaque(wv & 0x0F0F0F0Fu);
+              hi[dnt][dw] = opaque((wv >> 4) & 0x0F0F0F0Fu);
+            }
+            bnxt[dnt][dw * 4 + dp] = pk_bf16(fmaf(s_, ubyte_f32<dp>(lo[dnt][dw]), b_), fmaf(s_, ubyte_f32<dp>(hi[dnt][dw]), b_));
+          } else {
+            if constexpr (dp == 0) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) c4[dnt][dw][c] = opaque((wv >> (2 * c)) & 0x03030303u);
+            }
+            constexpr int m = dp / 2, e = (dp % 2) * 2;
+            bnxt[dnt][dw * 8 + dp] = pk_bf16(fmaf(s_, ubyte_f32<m>(c4[dnt][dw][e]), b_), fmaf(s_, ubyte_f32<m>(c4[dnt][dw][e + 1]), b_));
+          }
+        }
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    xs = xs1;
+    ws1 = ws2;
+  };
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, bA, bB, wA, wB);
+    step(kt + 1, bB, bA, wB, wA);
+  }
+  if (kt < nk) {
+    step(kt, bA, bB, wA, wB);
+  }
+
+  // epilogue: the accumulator of (mt, nt) is y^T: lane holds row m = col of
+  // the mt tile and columns 8*(i/4) + 4*h + (i%4) of the nt tile, i.e. four
+  // runs of 4 consecutive outputs, stored as one 8-byte (bf16) or 16-byte
+  // (f32 split partial) store each when N % 4 == 0.  A split writes its f32
+  // partial instead (one uniform branch around the whole store loop keeps the
+  // accumulators in registers).
+  const bool vec = (p.N & 3) == 0;
+  auto store = [&](auto put4, auto put1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 32 + col;
+      if (m >= M) continue;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = nt0 + (wn * NT + nt) * 32 + 8 * g + 4 * h;
+          const f32x16& a = acc[mt][nt];
+          if (vec && n + 3 < p.N) {
+            put4(m, n, a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) put1(m, n + e, a[4 * g + e]);
+          }
+        }
+    }
+  };
+  if constexpr (SPLIT) {
+    float* part = p.partial + (int64_t)split * M * p.N;
+    store([&](int m, int n, float v0, float v1, float v2, float v3) {
+            *reinterpret_cast<f32x4*>(part + (int64_t)m * p.N + n) = f32x4{v0, v1, v2, v3};
+          },
+          [&](int m, int n, float v) { part[(int64_t)m * p.N + n] = v; });
+  } else {
+    store([&](int m, int n, float v0, float v1, float v2, float v3) {
+            *reinterpret_cast<u32x2*>(y + (int64_t)m * p.N + n) = u32x2{pk_bf16(v0, v1), pk_bf16(v2, v3)};
+          },
+          [&](int m, int n, float v) { y[(int64_t)m * p.N + n] = f2bf(v); });
+  }
+}
+
+typedef void (*qmm_fn)(QmmParams);
+
+// Kernel of one (bits, split) quarter: qmm_k<bits>_<split>.hip instantiate the
+// tile heights MT = 4, 6, 8 and group sizes 32, 64, 128 (eight waves, NT = 1),
+// so the four quarters compile in parallel.  *lds = dynamic LDS bytes.
+template <int BITS, bool SPLIT>
+qmm_fn qmm_get(int gs, int MT, int* lds);
+
+template <int BITS, bool SPLIT>
+qmm_fn qmm_get_impl(int gs, int MT, int* lds) {
+  auto one = [&](auto mt) -> qmm_fn {
+    constexpr int M_ = decltype(mt)::value;
+    *lds = QmmLds<BITS, 64, M_, 1, 8>::TOTAL;  // (group-size independent)
+    if (gs == 32) return qmm_kernel<BITS, 32, M_, 1, 8, SPLIT>;
+    if (gs == 64) return qmm_kernel<BITS, 64, M_, 1, 8, SPLIT>;
+    if (gs == 128) return qmm_kernel<BITS, 128, M_, 1, 8, SPLIT>;
+    return nullptr;
+  };
+  if (MT == 8) return one(std::integral_constant<int, 8>{});
+  if (MT == 6) return one(std::integral_constant<int, 6>{});
+  if (MT == 4) return one(std::integral_constant<int, 4>{});
+  return nullptr;
+}
+
+}  // namespace lisaq
