@@ -36,6 +36,7 @@ struct QmvConfig {
                   // 4: persistent one-row dot kernel (U = passes, S = ring depth, S_inner = chunks)
   int tile_rows;  // rows of W per workgroup (32 or 16)
   int U, MQ, NW, S, S_inner, slab_groups, tiles, lds_bytes;
+  int tpb;  // streaming kernel: 16-row tiles per block (0 or 1: one)
   int MR;         // streaming kernel: accumulator rows per lane group in use (1, 2 or 4)
   int sbi;        // dot kernel: scale/bias staging loads per thread
   int sbw;        // one-row kernel: bytes per lane of the scale/bias row loads

@@ -131,8 +131,11 @@ __host__ __device__ inline QmvtLds qmvt_layout(int SG, int GS, int M, int MQ, in
   return L;
 }
 
+// NW waves per 16-row tile; a workgroup holds blockDim.x / (64 NW) tiles side
+// by side (tiles per block, 1 for tile-table launches), which share the
+// staged x: fewer x stagings per row at several rows of x.
 template <int BITS, int GS, int MQ, int MR, int SB, int NW, int D>
-__global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
+__global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
   constexpr int PACK = 32 / BITS;
   constexpr int GB = GS * BITS / 8;      // bytes of one group in a row
   constexpr int GPS = SB / GB;           // groups per W slab
@@ -149,6 +152,8 @@ __global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int tpb = blockDim.x / (64 * NW);  // tiles per block
+  const int wt = wave / NW, wl = wave - wt * NW;  // tile in the block, wave in the tile
   const int col = lane & 15;  // row n of the tile / row m of x in the A operand
   const int q = lane >> 4;    // lane group
 
@@ -157,7 +162,7 @@ __global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
   const uint16_t* bi = p.b;
   const uint16_t* x = p.x;
   uint16_t* y = p.y;
-  int n0 = blockIdx.x * 16;
+  int n0 = (blockIdx.x * tpb + wt) * 16;
   int M = p.M;
   if (p.tiles) {
     const int4 t = p.tiles[blockIdx.x];
@@ -173,7 +178,7 @@ __global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
   }
   const int n = n0 + col;
   const int SG = p.slab_groups;
-  const QmvtLds L = qmvt_layout(SG, GS, p.M, MQ, BITS, NW, SB);
+  const QmvtLds L = qmvt_layout(SG, GS, p.M, MQ, BITS, NW * tpb, SB);
   const int RSX = (SG * GS * 2 + 64) / 16;  // x row stride (uint4)
   u32x4* xl = reinterpret_cast<u32x4*>(smem + L.x_off);
   f32x4v* xs4 = reinterpret_cast<f32x4v*>(smem + L.xs_off);
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
     const int g_begin = xsl * SG;
     const int GL = (p.G - g_begin) < SG ? (p.G - g_begin) : SG;
     const int nws = GL / GPS;  // W slabs in this x slab
-    const int mine = nws > wave ? (nws - wave + NW - 1) / NW : 0;
+    const int mine = nws > wl ? (nws - wl + NW - 1) / NW : 0;
 
     // x staging, part 1: issue this thread's first pass of x loads before
     // the weight ring, so x does not queue behind the weight stream
@@ -251,7 +256,7 @@ __global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
     SBV sring[D], bring[D];  // scales / biases of the slab's GPS groups, this lane's row
     auto load_slab = [&](int j, u32x4* dst, SBV& sv, SBV& bv) {
       int jj = j < mine ? j : mine - 1;
-      const int64_t gfirst = g_begin + (wave + NW * jj) * GPS;
+      const int64_t gfirst = g_begin + (wl + NW * jj) * GPS;
       sv = *reinterpret_cast<const SBV*>(srow + gfirst);
       bv = *reinterpret_cast<const SBV*>(brow + gfirst);
       const int64_t off = gfirst * GB;
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
           yacc[0][0] += (float)(v[1] & 1);
           continue;
         }
-        const int gs0 = (wave + NW * j) * GPS;  // first group of the slab (in the x slab)
+        const int gs0 = (wl + NW * j) * GPS;  // first group of the slab (in the x slab)
 #pragma unroll
         for (int gl = 0; gl < GPS; ++gl) {
           const int b = gl * GB + qb;
@@ -423,17 +428,17 @@ __global__ __launch_bounds__(64 * NW) void qmvt_kernel(QmvParams p) {
 #pragma unroll
       for (int ii = 0; ii < MR; ++ii) red[((wave * MQ + a) * 4 + ii) * 64 + lane] = yacc[a][ii];
     __syncthreads();
-    if (wave != 0) return;
+    if (wl != 0) return;
 #pragma unroll
     for (int a = 0; a < MQ; ++a)
 #pragma unroll
       for (int ii = 0; ii < MR; ++ii) {
-        float v = red[(a * 4 + ii) * 64 + lane];
-        for (int w2 = 1; w2 < NW; ++w2) v += red[((w2 * MQ + a) * 4 + ii) * 64 + lane];
+        float v = red[((wave * MQ + a) * 4 + ii) * 64 + lane];
+        for (int w2 = 1; w2 < NW; ++w2) v += red[(((wave + w2) * MQ + a) * 4 + ii) * 64 + lane];
         yacc[a][ii] = v;
       }
   }
-  if (wave != 0 || n >= p.N) return;
+  if (wl != 0 || n >= p.N) return;
 #pragma unroll
   for (int a = 0; a < MQ; ++a)
 #pragma unroll
@@ -484,7 +489,14 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   if (SG > G) SG = G;
   c.slab_groups = SG;
   c.S_inner = (G + SG - 1) / SG;
-  c.lds_bytes = qmvt_layout(SG, gs, (int)M, c.MQ, bits, c.NW, SB).total;
+  // two tiles per block when there are rows of x to share and tiles to spare
+  // (measured: faster at N = 17408 with 2-4 rows of x; slower at N = 9728, no gain at 8 rows)
+  c.tpb = (M >= 2 && M <= 4 && c.NW == 4 && c.tiles >= 1024) ? 2 : 1;
+  if (const char* env = getenv("LISAQ_QMVT_TPB")) {  // tuning: 1 or 2
+    const int v = atoi(env);
+    if (v == 1 || (v == 2 && c.NW <= 4)) c.tpb = v;
+  }
+  c.lds_bytes = qmvt_layout(SG, gs, (int)M, c.MQ, bits, c.NW * c.tpb, SB).total;
   c.ws_bytes = 0;
   c.kind = 2;
   c.tile_rows = 16;
@@ -492,7 +504,7 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
 }
 
 int qmvt_lds_bytes(const QmvConfig& c, int gs, int M, int bits) {
-  return qmvt_layout(c.slab_groups, gs, M, c.MQ, bits, c.NW, c.U).total;
+  return qmvt_layout(c.slab_groups, gs, M, c.MQ, bits, c.NW * (c.tpb > 0 ? c.tpb : 1), c.U).total;
 }
 
 typedef void (*qmvt_fn)(QmvParams);
@@ -539,7 +551,15 @@ int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes);
     if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmvt: LDS %d bytes: %s", c.lds_bytes, hipGetErrorString(e));
   }
-  hipLaunchKernelGGL(fn, dim3(grid_x), dim3(64 * c.NW), c.lds_bytes, stream, p);
+  // tile-table launches: one tile per block (the table gives each block its tile)
+  const int tpb = p.tiles ? 1 : (c.tpb > 0 ? c.tpb : 1);
+  int lds = c.lds_bytes;
+  if (tpb != c.tpb) lds = qmvt_layout(c.slab_groups, gs, p.M, c.MQ, bits, c.NW * tpb, c.U).total;
+  if (lds > 64 * 1024 && lds != c.lds_bytes) {
+    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmvt: LDS %d bytes: %s", lds, hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(fn, dim3((grid_x + tpb - 1) / tpb), dim3(64 * c.NW * tpb), lds, stream, p);
   return check_launch("qmvt");
 }
 
