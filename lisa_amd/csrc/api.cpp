@@ -291,10 +291,14 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
   // row the arithmetic of an independent M=1 call.
   const QmvConfig c = qmv_config(1, N, K, gs, bits);
   if (c.kind == 4) {
-    // the one-row kernel: one launch per row
-    for (int64_t r = 0; r < M; ++r) {
-      rc = run_qmv((hipStream_t)stream, c, (const uint16_t*)x + r * K, w, s, b, (uint16_t*)y + r * N, 1, N, K, gs,
-                   bits, ws, ws_bytes);
+    // the persistent kernel computes each of its (one or two) rows with the
+    // one-row arithmetic, so pairs of rows share one pass over W
+    for (int64_t r = 0; r < M; r += 2) {
+      const int64_t mr = M - r < 2 ? M - r : 2;
+      const QmvConfig cp = mr == 1 ? c : qmvp_config(2, N, K, gs, bits);
+      if (cp.kind != 4) return set_error(LISAQ_EUNSUPPORTED, "serial_rows: no two-row persistent kernel");
+      rc = run_qmv((hipStream_t)stream, cp, (const uint16_t*)x + r * K, w, s, b, (uint16_t*)y + r * N, mr, N, K,
+                   gs, bits, ws, ws_bytes);
       if (rc) return rc;
     }
     return LISAQ_OK;

@@ -507,10 +507,10 @@ QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool s
 QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
   const char* force = getenv("LISAQ_QMV_KERNEL");  // tuning: "32", "16", "t" (streaming), "d" (dot), "p" (persistent)
   const char f = force ? force[0] : 0;
-  // One row: the persistent kernel when there are enough rows to keep every
-  // wave busy (measured), else the workgroup dot kernel; more rows: the MFMA
-  // streaming kernel.
-  if (!single_pass && f != '3' && f != '1' && f != 't' && f != 'd' && M == 1 && (N >= 16384 || f == 'p')) {
+  // One or two rows: the persistent kernel when there are enough rows to keep
+  // every wave busy (measured), else (one row) the workgroup dot kernel; more
+  // rows: the MFMA streaming kernel.
+  if (!single_pass && f != '3' && f != '1' && f != 't' && f != 'd' && M <= 2 && (N >= 16384 || f == 'p')) {
     const QmvConfig c = qmvp_config(M, N, K, gs, bits);
     if (c.kind == 4) return c;
   }

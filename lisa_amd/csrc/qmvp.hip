@@ -37,7 +37,10 @@ namespace lisaq {
 
 using namespace qmvdev;
 
-template <int BITS, int GS, int J, int D, int SBW>
+// MR rows of x (1 or 2) share the weight stream: each W word is unpacked once
+// and dotted with every row's x; each row's arithmetic is exactly the one-row
+// kernel's (same lanes, same order), so its result is bitwise the same.
+template <int BITS, int GS, int J, int D, int SBW, int MR>
 __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
   // SBW: bytes per lane of the two loads that bring a row's scales and
   // biases (lanes [0, SBL)); they pass through LDS to the lanes that use them
@@ -57,21 +60,21 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
   const uint32_t rowbytes = (uint32_t)C * CB;
   const int cnt = gw < N ? (N - 1 - gw) / nwv + 1 : 0;  // rows of this wave
   extern __shared__ float lds_res[];
-  float* res = lds_res + wave * p.tile_rows;  // p.tile_rows >= cnt
+  float* res = lds_res + wave * p.tile_rows * MR;  // [MR][p.tile_rows], p.tile_rows >= cnt
   const int G2 = (2 * G + 15) & ~15;          // bytes of one staged s (or b) row, padded
-  unsigned char* sbl = reinterpret_cast<unsigned char*>(lds_res + (blockDim.x >> 6) * p.tile_rows) + wave * 2 * G2;
+  unsigned char* sbl = reinterpret_cast<unsigned char*>(lds_res + (blockDim.x >> 6) * p.tile_rows * MR) + wave * 2 * G2;
   const int SBL = (2 * G + SBW - 1) / SBW;    // lanes that load
   const bool sb_lane = lane < SBL;
   const uint32_t sb_off = (uint32_t)lane * SBW;
   unsigned char* sb_dst = sbl + sb_off;
 
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)p.K * 2);
-  const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y, (uint32_t)N * 2);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)p.K * 2 * MR);
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y, (uint32_t)N * 2 * MR);
 
   // --- x of the lane's chunks (issued first; paired after the first rows are in flight)
   uint32_t woff[J];  // byte offset of the chunk in a row
   int gofs[J];       // byte offset of its group's scale in a staged row (0 past the row)
-  uint32_t raw[J][16];
+  uint32_t raw[MR][J][16];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int c = lane + 64 * j;
@@ -79,14 +82,17 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
     woff[j] = ok ? (uint32_t)c * CB : kOob;
     gofs[j] = ok ? (c * 32 / GS) * 2 : 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 v = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (ok && !PDBG(32)) ? (uint32_t)c * 64 + 16 * i : kOob, 0, 0));
-      raw[j][4 * i] = v[0];
-      raw[j][4 * i + 1] = v[1];
-      raw[j][4 * i + 2] = v[2];
-      raw[j][4 * i + 3] = v[3];
-    }
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 v = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rx, (ok && !PDBG(32)) ? (uint32_t)r * p.K * 2 + (uint32_t)c * 64 + 16 * i : kOob, 0, 0));
+        raw[r][j][4 * i] = v[0];
+        raw[r][j][4 * i + 1] = v[1];
+        raw[r][j][4 * i + 2] = v[2];
+        raw[r][j][4 * i + 3] = v[3];
+      }
   }
 
   // --- ring of D rows in flight
@@ -122,38 +128,13 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) issue(d, d);
 
-  // --- x paired in unpack order, with sums
-  uint32_t xp[J][NP];
-  float sx[J], st[J];
+  // --- x paired in unpack order, with sums (per row of x)
+  uint32_t xp[MR][J][NP];
+  float sx[MR][J], st[MR][J];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    auto xval = [&](int k) -> uint32_t { return (k & 1) ? (raw[j][k >> 1] >> 16) : (raw[j][k >> 1] & 0xffffu); };
-    sx[j] = 0.f;
-    st[j] = 0.f;
+  for (int r = 0; r < MR; ++r)
 #pragma unroll
-    for (int wd = 0; wd < WPC; ++wd)
-#pragma unroll
-      for (int q = 0; q < PPW; ++q) {
-        uint32_t lo, hi;
-        if constexpr (BITS == 4) {
-          lo = xval(8 * wd + q);
-          hi = xval(8 * wd + q + 4);
-          sx[j] += __uint_as_float(lo << 16) + __uint_as_float(hi << 16);
-        } else {
-          const int fq = q % 3;
-          const float f = fq == 0 ? 1.0f : (fq == 1 ? 0.25f : 0.0625f);
-          const float a = __uint_as_float(xval(16 * wd + q) << 16);
-          const float b = __uint_as_float(xval(16 * wd + q + 8) << 16);
-          sx[j] += a + b;
-          const float as = a * f, bs = b * f;  // power of two: exact
-          st[j] += as + bs;
-          lo = __float_as_uint(as) >> 16;
-          hi = __float_as_uint(bs) >> 16;
-        }
-        xp[j][wd * PPW + q] = lo | (hi << 16);
-      }
-    if constexpr (BITS == 4) st[j] = sx[j];
-  }
+    for (int j = 0; j < J; ++j) pair_x<BITS>(raw[r][j], xp[r][j], sx[r][j], st[r][j]);
 
   PConst kc;
   kc.init();
@@ -163,32 +144,42 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
       *reinterpret_cast<sbv_t*>(sb_dst) = sv[slot];
       *reinterpret_cast<sbv_t*>(sb_dst + G2) = bv[slot];
     }
-    float part = 0.f;
+    float part[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) part[r] = 0.f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      float d0 = 0.f, d1 = 0.f;
+      float d0[MR], d1[MR];
+#pragma unroll
+      for (int r = 0; r < MR; ++r) d0[r] = d1[r] = 0.f;
 #pragma unroll
       for (int wd = 0; wd < WPC; ++wd) {
         if (PDBG(2)) {  // skip the arithmetic
-          d0 += __uint_as_float(wv[slot][j][wd] & 0x3fffffu);
+          d0[0] += __uint_as_float(wv[slot][j][wd] & 0x3fffffu);
           continue;
         }
-        uint32_t r[PPW];
-        punpack<BITS>(wv[slot][j][wd], kc, r);
+        uint32_t rq[PPW];
+        punpack<BITS>(wv[slot][j][wd], kc, rq);
 #pragma unroll
-        for (int q = 0; q < PPW; ++q) {
-          if (q & 1) d1 = pdot2(r[q], xp[j][wd * PPW + q], d1);
-          else d0 = pdot2(r[q], xp[j][wd * PPW + q], d0);
-        }
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int q = 0; q < PPW; ++q) {
+            if (q & 1) d1[r] = pdot2(rq[q], xp[r][j][wd * PPW + q], d1[r]);
+            else d0[r] = pdot2(rq[q], xp[r][j][wd * PPW + q], d0[r]);
+          }
       }
       const float s = bf2f(*reinterpret_cast<const uint16_t*>(sbl + gofs[j]));
       const float b = bf2f(*reinterpret_cast<const uint16_t*>(sbl + G2 + gofs[j]));
-      part = fmaf(s, (d0 + d1) - 128.0f * st[j], fmaf(b, sx[j], part));
+#pragma unroll
+      for (int r = 0; r < MR; ++r) part[r] = fmaf(s, (d0[r] + d1[r]) - 128.0f * st[r][j], fmaf(b, sx[r][j], part[r]));
     }
-    const float total = wave_sum(part);
-    // results wait in LDS: a store here would be a vector-memory event
-    // between the ring's loads and blur the compiler's exact wait counts
-    if (lane == 0 && k < cnt) res[k] = total;
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      const float total = wave_sum(part[r]);
+      // results wait in LDS: a store here would be a vector-memory event
+      // between the ring's loads and blur the compiler's exact wait counts
+      if (lane == 0 && k < cnt) res[r * p.tile_rows + k] = total;
+    }
   };
 
   for (int k0 = 0; k0 < cnt; k0 += D) {
@@ -199,21 +190,26 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
     }
   }
   // (a wave's LDS operations complete in order: lane 0's writes are visible)
-  for (int k = lane; k < cnt; k += 64)
-    __builtin_amdgcn_raw_buffer_store_b16(f2bf(res[k]), ry, (uint32_t)(gw + k * nwv) * 2, 0, 0);
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+    for (int k = lane; k < cnt; k += 64)
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(res[r * p.tile_rows + k]), ry,
+                                            (uint32_t)(r * N + gw + k * nwv) * 2, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
 QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   QmvConfig c{};
   c.kind = -1;
-  if (M != 1 || (bits != 2 && bits != 4) || K % 32 != 0) return c;
+  if (M < 1 || M > 2 || (bits != 2 && bits != 4) || K % 32 != 0) return c;
   if (!(bits == 4 ? (gs == 32 || gs == 64 || gs == 128) : (gs == 64 || gs == 128))) return c;
   const int64_t C = K / 32;
   if (C > 192) return c;
   const int64_t rowbytes = C * (bits == 4 ? 16 : 8);
-  if (N * rowbytes >= (int64_t)kOob || N * (K / gs) * 2 >= (int64_t)kOob || K * 2 >= (int64_t)kOob) return c;
-  c.MR = 1;
+  if (N * rowbytes >= (int64_t)kOob || N * (K / gs) * 2 >= (int64_t)kOob || K * 2 * M >= (int64_t)kOob ||
+      N * 2 * M >= (int64_t)kOob)
+    return c;
+  c.MR = (int)M;
   c.U = (int)((C + 63) / 64);  // J passes
   c.S = 2;                     // ring depth D
   if (const char* env = getenv("LISAQ_QMVP_D")) {
@@ -246,7 +242,7 @@ QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
     }
   if (c.sbw == 0) return c;
   const int64_t g2 = (2 * G + 15) & ~15;
-  c.lds_bytes = (int)(4 * 4 * c.tile_rows + 4 * 2 * g2);
+  c.lds_bytes = (int)(4 * 4 * c.tile_rows * M + 4 * 2 * g2);
   if (c.lds_bytes > 64 * 1024) return c;  // (kind stays -1)
   c.ws_bytes = 0;
   c.kind = 4;
@@ -255,37 +251,44 @@ QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
 
 typedef void (*qmvp_fn)(QmvParams);
 
-template <int BITS, int GS, int J, int D>
+template <int BITS, int GS, int J, int D, int MR>
 static qmvp_fn qmvp_pick_w(int w) {
-  if (w == 16) return qmvp_kernel<BITS, GS, J, D, 16>;
-  if (w == 4) return qmvp_kernel<BITS, GS, J, D, 4>;
+  if (w == 16) return qmvp_kernel<BITS, GS, J, D, 16, MR>;
+  if (w == 4) return qmvp_kernel<BITS, GS, J, D, 4, MR>;
+  return nullptr;
+}
+
+template <int BITS, int GS, int J, int D>
+static qmvp_fn qmvp_pick_mr(int mr, int w) {
+  if (mr == 1) return qmvp_pick_w<BITS, GS, J, D, 1>(w);
+  if (mr == 2) return qmvp_pick_w<BITS, GS, J, D, 2>(w);
   return nullptr;
 }
 
 template <int BITS, int GS, int J>
-static qmvp_fn qmvp_pick_d(int d, int w) {
-  if (d == 2) return qmvp_pick_w<BITS, GS, J, 2>(w);
-  if (d == 3) return qmvp_pick_w<BITS, GS, J, 3>(w);
+static qmvp_fn qmvp_pick_d(int d, int mr, int w) {
+  if (d == 2) return qmvp_pick_mr<BITS, GS, J, 2>(mr, w);
+  if (d == 3) return qmvp_pick_mr<BITS, GS, J, 3>(mr, w);
   return nullptr;
 }
 
 template <int BITS, int GS>
-static qmvp_fn qmvp_pick(int j, int d, int w) {
-  if (j == 1) return qmvp_pick_d<BITS, GS, 1>(d, w);
-  if (j == 2) return qmvp_pick_d<BITS, GS, 2>(d, w);
-  if (j == 3) return qmvp_pick_d<BITS, GS, 3>(d, w);
+static qmvp_fn qmvp_pick(int j, int d, int mr, int w) {
+  if (j == 1) return qmvp_pick_d<BITS, GS, 1>(d, mr, w);
+  if (j == 2) return qmvp_pick_d<BITS, GS, 2>(d, mr, w);
+  if (j == 3) return qmvp_pick_d<BITS, GS, 3>(d, mr, w);
   return nullptr;
 }
 
 int qmvp_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
   qmvp_fn fn = nullptr;
-  if (bits == 4 && gs == 64) fn = qmvp_pick<4, 64>(c.U, c.S, c.sbw);
-  else if (bits == 4 && gs == 32) fn = qmvp_pick<4, 32>(c.U, c.S, c.sbw);
-  else if (bits == 4 && gs == 128) fn = qmvp_pick<4, 128>(c.U, c.S, c.sbw);
-  else if (bits == 2 && gs == 64) fn = qmvp_pick<2, 64>(c.U, c.S, c.sbw);
-  else if (bits == 2 && gs == 128) fn = qmvp_pick<2, 128>(c.U, c.S, c.sbw);
+  if (bits == 4 && gs == 64) fn = qmvp_pick<4, 64>(c.U, c.S, c.MR, c.sbw);
+  else if (bits == 4 && gs == 32) fn = qmvp_pick<4, 32>(c.U, c.S, c.MR, c.sbw);
+  else if (bits == 4 && gs == 128) fn = qmvp_pick<4, 128>(c.U, c.S, c.MR, c.sbw);
+  else if (bits == 2 && gs == 64) fn = qmvp_pick<2, 64>(c.U, c.S, c.MR, c.sbw);
+  else if (bits == 2 && gs == 128) fn = qmvp_pick<2, 128>(c.U, c.S, c.MR, c.sbw);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmvp: bits=%d gs=%d J=%d D=%d", bits, gs, c.U, c.S);
-  if (p.M != 1 || p.tiles) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: one plain row only");
+  if (p.M != c.MR || p.tiles) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: plain rows, configuration for M=%d", c.MR);
   if (p.K / 32 != c.S_inner) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: configuration made for another K");
   p.chunks = c.S_inner;
   p.tile_rows = c.tile_rows;
