@@ -14,16 +14,18 @@ struct QmmParams {
   int M, N, K, G;
   float* partial;       // split over K: [ksplit, M, N] f32 partial sums (plain launches only)
   int ksplit;           // K splits (1: the kernel writes y)
+  int full_tiles;       // split launches: whole tiles before the split units (0: every tile split)
 };
 
 struct QmmConfig {
   int MT, NT, WN, BM, BN, grid_n, grid_m;  // WN: waves along N (4 or 8), NT = 8 / WN
   int grid;  // workgroups of a plain (no tile table) launch: grid_n * grid_m
   int S;            // K splits of a plain launch (1: none)
+  int full_tiles;   // with S > 1: whole tiles before the split remainder (0: every tile split)
   size_t ws_bytes;  // workspace for the split partials (0 when S == 1)
 };
 
-QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool allow_split = true);
 // Enqueue.  A plain launch whose config splits K uses ws (>= c.ws_bytes) for
 // the partials, or runs unsplit when ws is missing or too small.
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,

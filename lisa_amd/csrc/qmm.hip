@@ -6,6 +6,25 @@
 
 namespace lisaq {
 
+// Remainder tiles of a hybrid launch: y = bf16(sum over the S parts), parts
+// added in order; unit (r, s) holds tile full_tiles + r's [BM][BN] partial.
+__global__ __launch_bounds__(256) void qmm_hybrid_reduce_kernel(const float* __restrict__ part,
+                                                                uint16_t* __restrict__ y, int M, int N, int BM,
+                                                                int BN, int gn, int full_tiles, int S,
+                                                                int64_t count) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int64_t tsz = (int64_t)BM * BN;
+  const int r = (int)(i / tsz), e = (int)(i - r * tsz);
+  const int tile = full_tiles + r;
+  const int m = (tile / gn) * BM + e / BN, n = (tile % gn) * BN + e % BN;
+  if (m >= M || n >= N) return;
+  const float* src = part + (int64_t)r * S * tsz + e;
+  float v = src[0];
+  for (int s = 1; s < S; ++s) v += src[s * tsz];
+  y[(int64_t)m * N + n] = f2bf(v);
+}
+
 // y = bf16(sum over the splits of the f32 partials), splits added in order.
 __global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __restrict__ part,
                                                                uint16_t* __restrict__ y, int64_t MN, int S) {
@@ -17,7 +36,7 @@ __global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __re
 }
 
 // ---------------------------------------------------------------------------
-QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool allow_split) {
   QmmConfig c{};
   // Row tile: 128, 192 or 256 rows (MT 32-row tiles), the one with the least
   // (rounds of 256 workgroups) x (rows per tile), i.e. the least matrix-core
@@ -35,6 +54,20 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
       }
     }
   }
+  // With at least one full round of 256-row tiles, 256-row tiles whatever
+  // the remainder (measured: a 256-row tile takes about the time of a
+  // 192-row one, the dequantized W operands serving more rows), and the
+  // remainder tiles split over K into a full last round (see below).
+  const int nk = (int)(K / 64);
+  bool hybrid = false;
+  {
+    const char* env = getenv("LISAQ_QMM_HYBRID");  // tuning: 0 disables
+    const int64_t t8 = ((N + 255) / 256) * ((M + 255) / 256);
+    if (allow_split && !(env && env[0] == '0') && t8 >= 256 && t8 % 256 != 0 && nk >= 16) {
+      c.MT = 8;
+      hybrid = true;
+    }
+  }
   c.WN = 8;
   if (const char* env = getenv("LISAQ_QMM_MT")) {  // tuning: 4, 6, 8
     const int v = atoi(env);
@@ -50,12 +83,27 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   // split K, up to about two workgroups per CU, each split at least 8
   // K-steps.  (Measured: at 136-160 tiles a split of 2 is already slower.)
   c.S = 1;
-  const int nk = (int)(K / 64);
-  if (c.grid < 128)
+  c.full_tiles = 0;
+  if (hybrid && c.MT == 8) {
+    // whole tiles for the full rounds, the R remaining tiles split into S
+    // parts (S <= 8, R * S <= 256, parts of at least 8 K-steps): f32 partials
+    // of the parts in the workspace, summed by qmm_hybrid_reduce_kernel
+    const int full = c.grid / 256 * 256, R = c.grid - full;
+    int S = 256 / R;
+    if (S > 8) S = 8;
+    while (S > 1 && nk / S < 8) --S;
+    if (S >= 2) {
+      c.full_tiles = full;
+      c.S = S;
+      c.ws_bytes = (size_t)R * S * c.BM * c.BN * 4;
+      return c;
+    }
+  }
+  if (c.grid < 128 && allow_split)
     while (c.grid * c.S * 2 <= 512 && nk / (c.S * 2) >= 8) c.S *= 2;
   if (const char* env = getenv("LISAQ_QMM_SPLIT")) {
     const int v = atoi(env);
-    if (v >= 1 && v <= nk) c.S = v;
+    if (v >= 1 && v <= nk && allow_split) c.S = v;
   }
   if (c.S > 1) {
     const int per = (nk + c.S - 1) / c.S;
@@ -76,8 +124,13 @@ static qmm_fn qmm_pick(const QmmConfig& c, int bits, int gs, int* lds) {
 
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
                int grid_y, void* ws, size_t ws_bytes) {
-  // split over K only for plain launches with room for the partials
+  // split over K only for plain launches with room for the partials (else the
+  // configuration without any split)
   const bool split = !p.tiles && c.S > 1 && ws != nullptr && ws_bytes >= c.ws_bytes;
+  if (!p.tiles && c.S > 1 && !split) {
+    const QmmConfig c1 = qmm_config(p.M, p.N, p.K, gs, bits, false);
+    return qmm_launch(stream, c1, p, bits, gs, c1.grid, grid_y, nullptr, 0);
+  }
   int lds = 0;
   qmm_fn fn = split ? qmm_pick<true>(c, bits, gs, &lds) : qmm_pick<false>(c, bits, gs, &lds);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);
@@ -88,9 +141,17 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
   LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
   p.ksplit = split ? c.S : 1;
   p.partial = split ? static_cast<float*>(ws) : nullptr;
-  hipLaunchKernelGGL(fn, dim3(split ? grid_x * c.S : grid_x, grid_y), dim3(64 * c.WN), lds, stream, p);
+  p.full_tiles = split ? c.full_tiles : 0;
+  const int grid = !split ? grid_x : (c.full_tiles > 0 ? c.full_tiles + (grid_x - c.full_tiles) * c.S : grid_x * c.S);
+  hipLaunchKernelGGL(fn, dim3(grid, grid_y), dim3(64 * c.WN), lds, stream, p);
   int rc = check_launch("qmm");
   if (rc || !split) return rc;
+  if (c.full_tiles > 0) {
+    const int64_t count = (int64_t)(grid_x - c.full_tiles) * c.BM * c.BN;
+    hipLaunchKernelGGL(qmm_hybrid_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)p.partial, p.y, p.M, p.N, c.BM, c.BN, c.grid_n, c.full_tiles, c.S, count);
+    return check_launch("qmm_hybrid_reduce");
+  }
   const int64_t MN = (int64_t)p.M * p.N;
   hipLaunchKernelGGL(qmm_split_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, stream,
                      (const float*)p.partial, p.y, MN, c.S);

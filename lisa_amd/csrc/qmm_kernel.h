@@ -180,7 +180,8 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   const uint16_t* x = p.x;
   uint16_t* y = p.y;
   int M = p.M;
-  int m0, nt0, split = 0;
+  int m0, nt0, split = 0, ksplit = p.ksplit, unit = -1;
+  bool whole = !SPLIT;  // (plain launches: every workgroup a whole tile)
   if (p.tiles) {
     const int4 t = p.tiles[blockIdx.x];
     if (t.x < 0) return;
@@ -194,11 +195,28 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
     m0 = 0;
     nt0 = t.w * BN;
   } else {
-    // row-block major: consecutive workgroups share an x row block and walk W;
-    // with a split over K, split s of every tile comes after split s-1's
+    // row-block major: consecutive workgroups share an x row block and walk W.
+    // Split launches: either every tile split over K (split s of every tile
+    // after split s-1's), or, with full_tiles > 0, the first full_tiles
+    // workgroups whole tiles and the rest the K-splits of the remaining tiles
+    // (unit u: tile full_tiles + u / ksplit, split u % ksplit), so that the
+    // last, partly filled round of whole tiles becomes a full round of parts.
     const int gn = (p.N + BN - 1) / BN, T = gn * ((M + BM - 1) / BM);
-    const int tile = blockIdx.x % T;
-    split = blockIdx.x / T;
+    int tile;
+    if (SPLIT && p.full_tiles > 0) {
+      if ((int)blockIdx.x < p.full_tiles) {
+        tile = blockIdx.x;
+        whole = true;
+        ksplit = 1;
+      } else {
+        unit = (int)blockIdx.x - p.full_tiles;
+        tile = p.full_tiles + unit / p.ksplit;
+        split = unit % p.ksplit;
+      }
+    } else {
+      tile = blockIdx.x % T;
+      split = blockIdx.x / T;
+    }
     nt0 = (tile % gn) * BN;
     m0 = (tile / gn) * BM;
   }
@@ -323,7 +341,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   // are constants.
   // K-steps of this workgroup: [kb, kb + nk) (the whole K unless split)
   const int nk_all = p.K / BK;
-  const int per = (nk_all + p.ksplit - 1) / p.ksplit;
+  const int per = (nk_all + ksplit - 1) / ksplit;
   const int kb = split * per;
   const int nk = nk_all - kb < per ? nk_all - kb : per;  // (host: every split has >= 1 step)
   auto kc = [&](int k) { return kb + (k < nk ? k : nk - 1); };
@@ -484,17 +502,26 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
         }
     }
   };
-  if constexpr (SPLIT) {
-    float* part = p.partial + (int64_t)split * M * p.N;
-    store([&](int m, int n, float v0, float v1, float v2, float v3) {
-            *reinterpret_cast<f32x4*>(part + (int64_t)m * p.N + n) = f32x4{v0, v1, v2, v3};
-          },
-          [&](int m, int n, float v) { part[(int64_t)m * p.N + n] = v; });
-  } else {
+  if (whole) {
     store([&](int m, int n, float v0, float v1, float v2, float v3) {
             *reinterpret_cast<u32x2*>(y + (int64_t)m * p.N + n) = u32x2{pk_bf16(v0, v1), pk_bf16(v2, v3)};
           },
           [&](int m, int n, float v) { y[(int64_t)m * p.N + n] = f2bf(v); });
+  } else if constexpr (SPLIT) {
+    if (unit >= 0) {
+      // compact partial of one unit: [BM][BN] f32 at unit * BM * BN
+      float* part = p.partial + (int64_t)unit * BM * BN;
+      store([&](int m, int n, float v0, float v1, float v2, float v3) {
+              *reinterpret_cast<f32x4*>(part + (m - m0) * BN + (n - nt0)) = f32x4{v0, v1, v2, v3};
+            },
+            [&](int m, int n, float v) { part[(m - m0) * BN + (n - nt0)] = v; });
+    } else {
+      float* part = p.partial + (int64_t)split * M * p.N;
+      store([&](int m, int n, float v0, float v1, float v2, float v3) {
+              *reinterpret_cast<f32x4*>(part + (int64_t)m * p.N + n) = f32x4{v0, v1, v2, v3};
+            },
+            [&](int m, int n, float v) { part[(int64_t)m * p.N + n] = v; });
+    }
   }
 }
 
