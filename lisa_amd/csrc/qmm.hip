@@ -8,21 +8,36 @@ namespace lisaq {
 
 // Remainder tiles of a hybrid launch: y = bf16(sum over the S parts), parts
 // added in order; unit (r, s) holds tile full_tiles + r's [BM][BN] partial.
+// Four consecutive columns per thread (16-byte part loads).
 __global__ __launch_bounds__(256) void qmm_hybrid_reduce_kernel(const float* __restrict__ part,
                                                                 uint16_t* __restrict__ y, int M, int N, int BM,
                                                                 int BN, int gn, int full_tiles, int S,
-                                                                int64_t count) {
+                                                                int64_t count4) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= count) return;
+  if (i >= count4) return;
   const int64_t tsz = (int64_t)BM * BN;
-  const int r = (int)(i / tsz), e = (int)(i - r * tsz);
+  const int64_t e4 = i * 4;
+  const int r = (int)(e4 / tsz), e = (int)(e4 - r * tsz);
   const int tile = full_tiles + r;
   const int m = (tile / gn) * BM + e / BN, n = (tile % gn) * BN + e % BN;
   if (m >= M || n >= N) return;
   const float* src = part + (int64_t)r * S * tsz + e;
-  float v = src[0];
-  for (int s = 1; s < S; ++s) v += src[s * tsz];
-  y[(int64_t)m * N + n] = f2bf(v);
+  f32x4 v = *reinterpret_cast<const f32x4*>(src);
+  for (int s = 1; s < S; ++s) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(src + s * tsz);
+    v[0] += t[0];
+    v[1] += t[1];
+    v[2] += t[2];
+    v[3] += t[3];
+  }
+  uint16_t* dst = y + (int64_t)m * N + n;
+  if (n + 3 < N && (N & 3) == 0) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{(uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
+                                           (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16)};
+  } else {
+    for (int c = 0; c < 4; ++c)
+      if (n + c < N) dst[c] = f2bf(v[c]);
+  }
 }
 
 // y = bf16(sum over the splits of the f32 partials), splits added in order.
@@ -147,9 +162,9 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
   int rc = check_launch("qmm");
   if (rc || !split) return rc;
   if (c.full_tiles > 0) {
-    const int64_t count = (int64_t)(grid_x - c.full_tiles) * c.BM * c.BN;
-    hipLaunchKernelGGL(qmm_hybrid_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,
-                       (const float*)p.partial, p.y, p.M, p.N, c.BM, c.BN, c.grid_n, c.full_tiles, c.S, count);
+    const int64_t count4 = (int64_t)(grid_x - c.full_tiles) * c.BM * c.BN / 4;
+    hipLaunchKernelGGL(qmm_hybrid_reduce_kernel, dim3((unsigned)((count4 + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)p.partial, p.y, p.M, p.N, c.BM, c.BN, c.grid_n, c.full_tiles, c.S, count4);
     return check_launch("qmm_hybrid_reduce");
   }
   const int64_t MN = (int64_t)p.M * p.N;
