@@ -95,8 +95,11 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool all
   c.grid_m = (int)((M + c.BM - 1) / c.BM);
   c.grid = c.grid_n * c.grid_m;  // 1-D launch (see the kernel's tile order)
   // Far too few tiles for the 256 CUs (e.g. N = 5120 at M = 128: 20 tiles):
-  // split K, up to about two workgroups per CU, each split at least 8
-  // K-steps.  (Measured: at 136-160 tiles a split of 2 is already slower.)
+  // split K into the most parts that still fit one round (one workgroup per
+  // CU: the LDS ring and two waves per SIMD take a CU), at most 16, each at
+  // least 8 K-steps.  (Measured: a second, mostly empty round of parts costs
+  // ~40%: M=128 x 17408 x 5120 at 4 parts = 272 workgroups 71 us, at 3 parts
+  // 50 us; at 136-160 tiles a split of 2 is slower.)
   c.S = 1;
   c.full_tiles = 0;
   if (hybrid && c.MT == 8) {
@@ -114,8 +117,12 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool all
       return c;
     }
   }
-  if (c.grid < 128 && allow_split)
-    while (c.grid * c.S * 2 <= 512 && nk / (c.S * 2) >= 8) c.S *= 2;
+  if (c.grid < 128 && allow_split) {
+    int S = 256 / c.grid;
+    if (S > 16) S = 16;
+    while (S > 1 && nk / S < 8) --S;
+    c.S = S;
+  }
   if (const char* env = getenv("LISAQ_QMM_SPLIT")) {
     const int v = atoi(env);
     if (v >= 1 && v <= nk && allow_split) c.S = v;
