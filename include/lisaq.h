@@ -162,7 +162,7 @@ LISAQ_API int lisaq_moe_combine(void* stream, const void* down_sorted, const flo
  * topk_idx/topk_weights [T,k] may be NULL.
  * Few tokens (lisaq_moe_decode_supported: T <= 8, the engine's decode window,
  * moe.rs:263-332, 415-420) take the fused decode path of moe_decode.rs
- * (gate|up + SwiGLU, then down + combine: two launches after the router),
+ * (routing + gate|up + SwiGLU, then down + combine: two launches),
  * with the same rounding points; the environment variable LISAQ_MOE_FUSED=0
  * selects the generic path instead.
  * workspace: lisaq_moe_workspace() bytes, zero-filled before first use. */
@@ -176,8 +176,9 @@ LISAQ_API size_t lisaq_moe_workspace(int64_t T, int64_t H, int64_t I, int E, int
                            int bits);
 /* 1 if lisaq_moe_forward takes the fused decode path for these sizes: T <= 8,
  * H and I multiples of 32 and of group_size, H <= 8192, k in {1,2,4,8,16},
- * bits 2 or 4; else 0. */
-LISAQ_API int lisaq_moe_decode_supported(int64_t T, int64_t H, int64_t I, int k, int group_size, int bits);
+ * k <= E <= 1024, bits 2 or 4; else 0. */
+LISAQ_API int lisaq_moe_decode_supported(int64_t T, int64_t H, int64_t I, int E, int k, int group_size,
+                                         int bits);
 
 /* ---- layout helpers (host only, no device work) -------------------------
  * detect_group_size (EQ:273-287): gs = (weight_cols*32/bits)/scales_cols when

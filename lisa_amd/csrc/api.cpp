@@ -192,8 +192,8 @@ int lisaq_version(void) { return 100; }
 
 const char* lisaq_last_error(void) { return g_err; }
 
-int lisaq_moe_decode_supported(int64_t T, int64_t H, int64_t I, int k, int gs, int bits) {
-  return moe_decode_supported(T, H, I, k, gs, bits) ? 1 : 0;
+int lisaq_moe_decode_supported(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
+  return moe_decode_supported(T, H, I, E, k, gs, bits) ? 1 : 0;
 }
 
 int lisaq_qmv_batch_limit(int64_t K, int64_t N) {
@@ -500,18 +500,18 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   void* gws = B + L.gws;
   const size_t gws_bytes = L.total - L.gws;
   int rc;
-  if ((rc = lisaq_moe_route(st, logits, T, E, k, idx, wts))) return rc;
   // Few tokens (T <= 8, the reference's decode window): fused path, two
-  // launches after the router (LISAQ_MOE_FUSED=0 selects the generic path)
+  // launches, the first one routing (LISAQ_MOE_FUSED=0 selects the generic path)
   const char* fenv = getenv("LISAQ_MOE_FUSED");
-  if (!(fenv && fenv[0] == '0') && moe_decode_supported(T, H, I, k, gs, bits)) {
+  if (!(fenv && fenv[0] == '0') && moe_decode_supported(T, H, I, E, k, gs, bits)) {
     if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, out, R, H, I, 1, gs, bits))) return rc;
-    return launch_moe_decode(st, (const uint16_t*)x, idx, wts, gw, (const uint16_t*)gsc, (const uint16_t*)gbi, uw,
+    return launch_moe_decode(st, (const uint16_t*)x, logits, idx, wts, gw, (const uint16_t*)gsc, (const uint16_t*)gbi, uw,
                              (const uint16_t*)usc, (const uint16_t*)ubi, dw, (const uint16_t*)dsc,
                              (const uint16_t*)dbi, g, (uint16_t*)out, T, H, I, E, k, gs, bits);
   }
+  if ((rc = lisaq_moe_route(st, logits, T, E, k, idx, wts))) return rc;
   LISAQ_REQUIRE(E <= 1024, LISAQ_EINVAL_SHAPE, "moe_forward: need E <= 1024 (E=%d)", E);
   if ((rc = launch_sort_parallel(st, idx, R, E, k, sorted, order, rows, inv, offs, (int32_t*)(B + L.hist))))
     return rc;

@@ -17,9 +17,9 @@ int launch_gather_rows(hipStream_t st, const uint16_t* x, const int32_t* rows, u
 int launch_swiglu(hipStream_t st, const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n);
 int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const int32_t* inv,
                    uint16_t* out, int64_t T, int k, int64_t H);
-// fused decode MoE (moe_decode.hip): gate|up + SwiGLU, then down + combine
-bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int k, int gs, int bits);
-int launch_moe_decode(hipStream_t st, const uint16_t* x, const int32_t* idx, const float* wts,
+// fused decode MoE (moe_decode.hip): routing + gate|up + SwiGLU, then down + combine
+bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits);
+int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, int32_t* idx, float* wts,
                       const uint32_t* gw, const uint16_t* gsc, const uint16_t* gbi, const uint32_t* uw,
                       const uint16_t* usc, const uint16_t* ubi, const uint32_t* dw, const uint16_t* dsc,
                       const uint16_t* dbi, uint16_t* act, uint16_t* out, int64_t T, int64_t H, int64_t I, int E,

@@ -20,24 +20,6 @@ namespace lisaq {
 // found with one ballot per expert slot.  (A NaN logit counts as -inf.)
 // Softmax over the k selected logits in f32: e = exp(l - max), the sum in
 // round order, w = e * (1/sum) (softmax_single_row's normalizer).
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float route_dpp(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY),
-                                                               __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF,
-                                                               false));
-}
-// wave maximum, broadcast (lane 63 collects rows 0..3 through the row
-// broadcasts, then readlane)
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, route_dpp<0xB1, 0xF>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, route_dpp<0x4E, 0xF>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, route_dpp<0x141, 0xF>(v));  // row_half_mirror
-  v = fmaxf(v, route_dpp<0x140, 0xF>(v));  // row_mirror: every lane holds its row's max
-  v = fmaxf(v, route_dpp<0x142, 0xA>(v));  // row_bcast15
-  v = fmaxf(v, route_dpp<0x143, 0xC>(v));  // row_bcast31
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
 template <int PER>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int64_t T,
                                                     int E, int k, int32_t* __restrict__ idx,
@@ -45,54 +27,12 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   const int lane = threadIdx.x & 63;
   const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const float* l = logits + t * E;
-  float v[PER];
-  uint32_t taken = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e = lane + 64 * i;
-    const float x = e < E ? l[e] : -INFINITY;
-    v[i] = x != x ? -INFINITY : x + 0.0f;  // NaN -> -inf; -0 -> +0
-    if (e >= E) taken |= 1u << i;
-  }
-  // lane r keeps round r's winner (k <= 64)
-  float mysel = -INFINITY;
-  int mysid = 0;
-  for (int r = 0; r < k; ++r) {
-    // lane-local best not yet taken (scanning upward keeps the lowest slot on ties)
-    float best = -INFINITY;
-    int bslot = -1;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const bool ok = !(taken & (1u << i)) && (bslot < 0 || v[i] > best);
-      best = ok ? v[i] : best;
-      bslot = ok ? i : bslot;
-    }
-    const float m = wave_max(bslot >= 0 ? best : -INFINITY);
-    // the lowest expert id with value m: lowest slot, then lowest lane
-    int win = -1;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const uint64_t bal = __ballot(bslot == i && best == m);
-      if (win < 0 && bal != 0) win = i * 64 + (int)__builtin_ctzll(bal);
-    }
-    if (win < 0) win = 0;  // (only when fewer than k experts remain; k <= E is checked on the host)
-    if ((win & 63) == lane) taken |= 1u << (win >> 6);
-    if (lane == r) {
-      mysel = m;
-      mysid = win;
-    }
-  }
-  // softmax over the k selected logits: max, then exp and the sum in round
-  // order, w = e * (1/sum)
-  const float mx = wave_max(lane < k ? mysel : -INFINITY);
-  const float ex = lane < k ? expf(mysel - mx) : 0.f;
-  float sum = 0.f;
-  for (int r = 0; r < k; ++r) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
-  const float inv = 1.0f / sum;
+  int sid;
+  float w;
+  route_wave<PER>(logits + t * E, E, k, lane, sid, w);
   if (lane < k) {
-    idx[t * k + lane] = mysid;
-    wts[t * k + lane] = ex * inv;
+    idx[t * k + lane] = sid;
+    wts[t * k + lane] = w;
   }
 }
 

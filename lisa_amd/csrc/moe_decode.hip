@@ -16,6 +16,8 @@
 // RPW rows of I; a lane owns the 32-code chunks lane, lane+64, ... of the H
 // inputs, so one 16-byte load per lane and row reads a whole 1 KB row slice
 // and x stays in registers; all RPW rows' loads are issued before any math.
+// The gate|up kernel also routes: every wave computes its token's top-k from
+// the router logits (the router's arithmetic), so the path is two launches.
 // down_combine: each wave RPW output rows of H; the k experts of the token are
 // side by side in the wave (64/k lanes per expert row), the partial dot
 // products are summed within each lane group, and the k results are folded
@@ -33,8 +35,9 @@ namespace {
 
 struct MoeDecodeParams {
   const uint16_t* x;    // [T, H] bf16
-  const int32_t* idx;   // [T*k] expert ids in slot order t*k + j
-  const float* wts;     // [T*k] routing weights
+  const float* logits;  // [T, E] router logits (gate|up kernel: routes each token itself)
+  int32_t* idx;         // [T*k] expert ids in slot order t*k + j (written by the gate|up kernel)
+  float* wts;           // [T*k] routing weights
   const uint32_t *gw, *uw, *dw;                 // [E, I, H/pack], [E, I, H/pack], [E, H, I/pack]
   const uint16_t *gsc, *gbi, *usc, *ubi, *dsc, *dbi;
   uint16_t* act;        // [T*k, I] bf16
@@ -65,16 +68,14 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* p, uint32_t* raw) {
   }
 }
 
-template <int BITS, int GS, int J>
+template <int BITS, int GS, int J, int PER>
 __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p) {
   constexpr int PACK = 32 / BITS, WPC = 32 / PACK;  // words per chunk
   constexpr int NP = WPC * (16 / BITS);             // pairs per chunk
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int z = blockIdx.y;  // slot t*k + j
-  const int t = z / p.k;
-  const int e = p.idx[z];
-  const bool valid_e = e >= 0 && e < p.E;
+  const int t = z / p.k, jz = z - t * p.k;
   const int r0 = (blockIdx.x * 4 + wave) * RPW;
   if (r0 >= p.I) return;
   const int C = p.H / 32, G = p.H / GS;
@@ -89,6 +90,21 @@ __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p)
 #pragma unroll
       for (int i = 0; i < 16; ++i) raw[j][i] = 0;
   }
+  // the token's routing (every wave routes its token: no separate router
+  // launch); slot jz's expert.  One wave per token writes the ids and weights
+  // for the down kernel and the caller.
+  int e;
+  {
+    int sid;
+    float w;
+    route_wave<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, lane, sid, w);
+    e = __builtin_amdgcn_readlane(sid, jz);
+    if (blockIdx.x == 0 && wave == 0 && jz == 0 && lane < p.k) {
+      p.idx[(int64_t)t * p.k + lane] = sid;
+      p.wts[(int64_t)t * p.k + lane] = w;
+    }
+  }
+  const bool valid_e = e >= 0 && e < p.E;
   // every row's W words, scales and biases
   uint32_t wg_[RPW][J][WPC], wu_[RPW][J][WPC];
   uint16_t sg_[RPW][J], bg_[RPW][J], su_[RPW][J], bu_[RPW][J];
@@ -219,13 +235,18 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p
 
 typedef void (*moe_fn)(MoeDecodeParams);
 
-template <int BITS, int GS>
-moe_fn pick_gu(int J) {
-  if (J == 1) return moe_gate_up_act_kernel<BITS, GS, 1>;
-  if (J == 2) return moe_gate_up_act_kernel<BITS, GS, 2>;
-  if (J == 3) return moe_gate_up_act_kernel<BITS, GS, 3>;
-  if (J == 4) return moe_gate_up_act_kernel<BITS, GS, 4>;
+template <int BITS, int GS, int PER>
+moe_fn pick_gu_j(int J) {
+  if (J == 1) return moe_gate_up_act_kernel<BITS, GS, 1, PER>;
+  if (J == 2) return moe_gate_up_act_kernel<BITS, GS, 2, PER>;
+  if (J == 3) return moe_gate_up_act_kernel<BITS, GS, 3, PER>;
+  if (J == 4) return moe_gate_up_act_kernel<BITS, GS, 4, PER>;
   return nullptr;
+}
+
+template <int BITS, int GS>
+moe_fn pick_gu(int J, int E) {
+  return E <= 128 ? pick_gu_j<BITS, GS, 2>(J) : pick_gu_j<BITS, GS, 16>(J);
 }
 
 template <int BITS, int GS, int KE>
@@ -268,8 +289,9 @@ int down_passes(int64_t I, int k) { return (int)((I / 32 + 64 / k - 1) / (64 / k
 
 }  // namespace
 
-bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int k, int gs, int bits) {
+bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
   if (T < 1 || T > 8 || H % 32 || I % 32 || H > 4 * 64 * 32) return false;
+  if (E < k || E > 1024 || k > 32) return false;  // (in-kernel routing: E <= 1024, 1 <= k <= 32)
   if (!(k == 1 || k == 2 || k == 4 || k == 8 || k == 16)) return false;
   if (!(bits == 2 || bits == 4) || !(gs == 32 || gs == 64 || gs == 128)) return false;
   if (H % gs || I % gs) return false;
@@ -277,18 +299,18 @@ bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int k, int gs, int bi
   return P == 1 || P == 2 || P == 3 || P == 4 || P == 6 || P == 8;
 }
 
-int launch_moe_decode(hipStream_t st, const uint16_t* x, const int32_t* idx, const float* wts,
+int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, int32_t* idx, float* wts,
                       const uint32_t* gw, const uint16_t* gsc, const uint16_t* gbi, const uint32_t* uw,
                       const uint16_t* usc, const uint16_t* ubi, const uint32_t* dw, const uint16_t* dsc,
                       const uint16_t* dbi, uint16_t* act, uint16_t* out, int64_t T, int64_t H, int64_t I, int E,
                       int k, int gs, int bits) {
-  if (!moe_decode_supported(T, H, I, k, gs, bits))
+  if (!moe_decode_supported(T, H, I, E, k, gs, bits))
     return set_error(LISAQ_EUNSUPPORTED, "moe decode: T=%lld H=%lld I=%lld k=%d gs=%d bits=%d", (long long)T,
                      (long long)H, (long long)I, k, gs, bits);
-  MoeDecodeParams p{x, idx, wts, gw, uw, dw, gsc, gbi, usc, ubi, dsc, dbi, act, out, (int)T, (int)H, (int)I, E, k};
+  MoeDecodeParams p{x, logits, idx, wts, gw, uw, dw, gsc, gbi, usc, ubi, dsc, dbi, act, out, (int)T, (int)H, (int)I, E, k};
   const int J = (int)((H / 32 + 63) / 64);
   const int P = down_passes(I, k);
-  moe_fn gu = by_format(bits, gs, [&](auto B, auto S) { return pick_gu<decltype(B)::value, decltype(S)::value>(J); });
+  moe_fn gu = by_format(bits, gs, [&](auto B, auto S) { return pick_gu<decltype(B)::value, decltype(S)::value>(J, E); });
   moe_fn dc = by_format(bits, gs, [&](auto B, auto S) { return pick_dc<decltype(B)::value, decltype(S)::value>(k, P); });
   if (!gu || !dc) return set_error(LISAQ_EUNSUPPORTED, "moe decode: no kernel for J=%d P=%d k=%d", J, P, k);
   hipLaunchKernelGGL(gu, dim3((unsigned)((I + 4 * RPW - 1) / (4 * RPW)), (unsigned)(T * k)), dim3(256), 0, st, p);

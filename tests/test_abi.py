@@ -115,6 +115,10 @@ def test_workspace_queries():
     # every matvec runs in one pass per row tile (no cross-workgroup split): no workspace
     assert lib.lisaq_quantized_matmul_workspace(1, 17408, 5120, 64, 4) == 0
     assert lib.lisaq_quantized_matmul_workspace(8, 2560, 9728, 64, 4) == 0
-    assert lib.lisaq_quantized_matmul_workspace(2048, 17408, 5120, 64, 4) == 0
+    # matmul at M=2048, N=17408: 68 x 8 = 544 tiles of 256 x 256; the 32 past two full rounds of 256 CUs are
+    # split over K into 8 parts with f32 partials: 32 * 8 * 256 * 256 * 4 bytes
+    assert lib.lisaq_quantized_matmul_workspace(2048, 17408, 5120, 64, 4) == 32 * 8 * 256 * 256 * 4
+    # M=2048, N=5120: 8 x 20 = 160 tiles of 256 rows, fewer than one round: 192-row tiles, no split
+    assert lib.lisaq_quantized_matmul_workspace(2048, 5120, 17408, 64, 4) == 0
     assert lib.lisaq_gather_qmm_workspace(32768, 768, 2048, 128, 64, 4) >= 256
     assert lib.lisaq_moe_workspace(4096, 2048, 768, 128, 8, 64, 4) > 32768 * 2048 * 2

@@ -181,7 +181,7 @@ def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
     x = np_x(rng, T, H)
     lg = rng.standard_normal((T, E)).astype(np.float32)
     dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
-    assert _lib.load().lisaq_moe_decode_supported(T, H, I, k, gs, bits) == 1
+    assert _lib.load().lisaq_moe_decode_supported(T, H, I, E, k, gs, bits) == 1
     outs = {}
     for fused in ("1", "0"):
         monkeypatch.setenv("LISAQ_MOE_FUSED", fused)
