@@ -51,10 +51,10 @@ constexpr int RPW = 2;  // rows per wave (both kernels)
 template <int BITS>
 __device__ __forceinline__ void load_chunk(const uint32_t* p, uint32_t* w) {
   if constexpr (BITS == 4) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));  // read once
     w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
   } else {
-    const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
     w[0] = v[0]; w[1] = v[1];
   }
 }

@@ -16,6 +16,9 @@ __device__ __forceinline__ float pdot2(uint32_t a, uint32_t b, float c) {
 
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
 constexpr uint32_t kOob = 0x40000000u;  // past every buffer's range; two of them still fit in 32 bits
+// cache policy of loads that stream data read once (the weights of a matvec):
+// nontemporal (measured 4.5% faster on a 50 MB matvec than the default policy)
+constexpr int kNt = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
@@ -82,37 +85,51 @@ __device__ __forceinline__ float wave_sum(float v) {
 // half of raw[i]) paired in unpack order: xp[wd * PPW + q] holds the x of the
 // two codes that punpack<BITS> puts in pair q of word wd (2 bits: scaled by
 // 1, 1/4, 1/16 as the pair's code shift).  sx = sum of x, st = sum of the
-// scaled x (st = sx at 4 bits).
+// scaled x (st = sx at 4 bits); both are bf16 dot products with (1, 1), one
+// instruction per pair (the scaled values are exact in bf16: powers of two).
 template <int BITS>
 __device__ __forceinline__ void pair_x(const uint32_t* raw, uint32_t* xp, float& sx, float& st) {
   constexpr int WPC = BITS == 4 ? 4 : 2;  // words per chunk
   constexpr int PPW = 16 / BITS;          // pairs per word
+  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
   auto xval = [&](int k) -> uint32_t { return (k & 1) ? (raw[k >> 1] >> 16) : (raw[k >> 1] & 0xffffu); };
-  sx = 0.f;
-  st = 0.f;
 #pragma unroll
   for (int wd = 0; wd < WPC; ++wd)
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
       uint32_t lo, hi;
       if constexpr (BITS == 4) {
-        lo = xval(8 * wd + q);
-        hi = xval(8 * wd + q + 4);
-        sx += __uint_as_float(lo << 16) + __uint_as_float(hi << 16);
+        // x[8wd+q] and x[8wd+q+4] are the same halves of raw[4wd+q/2] and
+        // raw[4wd+q/2+2]: one byte permute
+        const uint32_t a = raw[4 * wd + q / 2], b = raw[4 * wd + q / 2 + 2];
+        xp[wd * PPW + q] = __builtin_amdgcn_perm(b, a, (q & 1) ? 0x07060302u : 0x05040100u);
+        continue;
       } else {
         const int fq = q % 3;
         const float f = fq == 0 ? 1.0f : (fq == 1 ? 0.25f : 0.0625f);
-        const float a = __uint_as_float(xval(16 * wd + q) << 16);
-        const float b = __uint_as_float(xval(16 * wd + q + 8) << 16);
-        sx += a + b;
-        const float as = a * f, bs = b * f;  // power of two: exact
-        st += as + bs;
-        lo = __float_as_uint(as) >> 16;
-        hi = __float_as_uint(bs) >> 16;
+        lo = __float_as_uint(__uint_as_float(xval(16 * wd + q) << 16) * f) >> 16;  // power of two: exact
+        hi = __float_as_uint(__uint_as_float(xval(16 * wd + q + 8) << 16) * f) >> 16;
       }
       xp[wd * PPW + q] = lo | (hi << 16);
     }
-  if constexpr (BITS == 4) st = sx;
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    a0 = pdot2(raw[i], kOnes, a0);
+    a1 = pdot2(raw[i + 1], kOnes, a1);
+  }
+  sx = a0 + a1;
+  if constexpr (BITS == 4) {
+    st = sx;
+  } else {
+    float t0 = 0.f, t1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < WPC * PPW; i += 2) {
+      t0 = pdot2(xp[i], kOnes, t0);
+      t1 = pdot2(xp[i + 1], kOnes, t1);
+    }
+    st = t0 + t1;
+  }
 }
 
 // sum(x * (128 + q)) of one chunk: the chunk's words w[WPC] against xp

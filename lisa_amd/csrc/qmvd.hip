@@ -197,7 +197,8 @@ __global__ __launch_bounds__(kQmvdMaxThreads) void qmvd_kernel(QmvParams p) {
     if (QDBG(8)) {  // skip the weight loads
       for (int j = 0; j < WPC; ++j) wv[i][j] = (uint32_t)(r * 77 + j);
     } else {
-      wv[i] = *reinterpret_cast<const chunk_t*>(reinterpret_cast<const unsigned char*>(w) + r * rowbytes + lc * CB);
+      wv[i] = __builtin_nontemporal_load(  // read once: nontemporal
+          reinterpret_cast<const chunk_t*>(reinterpret_cast<const unsigned char*>(w) + r * rowbytes + lc * CB));
     }
     // keep the issue order (x, s/b, then row by row) so each wait is exact
     __builtin_amdgcn_sched_barrier(0);

@@ -17,6 +17,7 @@
 // dropped by the hardware range check, so the loop body has no branches and
 // the compiler's waits are exact counts.  A row is finished with a fixed
 // butterfly over the 64 lanes (DPP within rows of 16 lanes, then lane swaps).
+// Weights, scales and biases are read once: nontemporal loads.
 // Codes become bf16 128+q with one v_and_or_b32 per pair (mantissa OR,
 // exact); v_dot2c_f32_bf16 forms sum(x*(128+q)) and the epilogue subtracts
 // 128*sum(x).  2-bit codes use masks 3/0xC/0x30 with x pre-scaled by
@@ -110,18 +111,18 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       if constexpr (WPC == 4)
-        wv[slot][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b128(rw, woff[j], 0, 0));
+        wv[slot][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b128(rw, woff[j], 0, kNt));
       else
-        wv[slot][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b64(rw, woff[j], 0, 0));
+        wv[slot][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b64(rw, woff[j], 0, kNt));
     }
     const uint32_t o = (sb_lane && !PDBG(1)) ? sb_off : kOob;  // (1: skip the scale/bias loads)
     static_assert(SBW == 16 || SBW == 4, "scale/bias load width");
     if constexpr (SBW == 16) {
-      sv[slot] = __builtin_bit_cast(sbv_t, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0));
-      bv[slot] = __builtin_bit_cast(sbv_t, __builtin_amdgcn_raw_buffer_load_b128(rb, o, 0, 0));
+      sv[slot] = __builtin_bit_cast(sbv_t, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kNt));
+      bv[slot] = __builtin_bit_cast(sbv_t, __builtin_amdgcn_raw_buffer_load_b128(rb, o, 0, kNt));
     } else {
-      sv[slot] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
-      bv[slot] = __builtin_amdgcn_raw_buffer_load_b32(rb, o, 0, 0);
+      sv[slot] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, kNt);
+      bv[slot] = __builtin_amdgcn_raw_buffer_load_b32(rb, o, 0, kNt);
     }
   };
 

@@ -67,6 +67,8 @@ def test_qmv_parity(dev, oracle, M, N, K, bits, gs):
     (1, 777, 2048, 2, 128),
     (2, 3001, 5120, 4, 64),
     (2, 640, 2048, 2, 64),
+    (2, 4097, 2560, 4, 32),     # four rows a step (K = 2560), ragged last step, two rows of x
+    (1, 1001, 5120, 4, 128),    # two rows a step (K = 5120), odd N
 ])
 def test_qmv_every_kernel(dev, oracle, monkeypatch, kernel, M, N, K, bits, gs):
     """Each matvec kernel (forced through LISAQ_QMV_KERNEL; a shape it does not
