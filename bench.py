@@ -11,7 +11,8 @@ timed.  The qmm figure (M=2048, TFLOP/s of 2*M*N*K) is reported beside it.
 
 ``cpu_baseline`` times the CPU oracle's fused dequant-dot (the reference's
 dequantize-then-matmul arithmetic, oracle/lisaq_oracle.c) on the host cores
-over a bounded number of calls of the same shape.
+over a bounded number of calls of the same shape; its ``materialize`` entry
+times the literal chain (W dequantized to f32, then an f32 product).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -289,7 +290,10 @@ def config_table(dev, gen, stream):
 
 
 def cpu_baseline(M, N, K, bits, gs, seconds):
-    """Oracle fused dequant-dot on host threads over a bounded number of calls."""
+    """Oracle on host threads over a bounded number of calls, two ways: the
+    fused dequant-dot (``value``: each weight decoded and used once), and the
+    reference's literal chain -- dequantize W to f32 (AO:56-83), then an f32
+    matrix-vector product (numpy/BLAS) -- under ``materialize``."""
     import numpy as np
 
     from lisa_amd.synth import np_linear, np_x
@@ -300,25 +304,30 @@ def cpu_baseline(M, N, K, bits, gs, seconds):
     w, s, b = np_linear(rng, N, K, bits, gs)
     x = np_x(rng, M, K)
     threads = min(16, os.cpu_count() or 1)
-    res = {}
-    for nt in (threads, 1):
-        budget = seconds * (0.75 if nt == threads else 0.25)
+    nbytes = qmv_bytes(M, N, K, bits, gs)
+
+    def timed(fn, budget, min_calls=1):
         calls, t0 = 0, time.perf_counter()
         while True:
-            O.qmv_threads(x, w, s, b, gs, bits, nt)
+            fn()
             calls += 1
             el = time.perf_counter() - t0
-            if el >= budget:
-                break
-        res[nt] = (calls, el)
-    calls, el = res[threads]
-    nbytes = qmv_bytes(M, N, K, bits, gs)
-    c1, e1 = res[1]
+            if el >= budget and calls >= min_calls:
+                return calls, el
+
+    calls, el = timed(lambda: O.qmv_threads(x, w, s, b, gs, bits, threads), seconds * 0.6)
+    c1, e1 = timed(lambda: O.qmv_threads(x, w, s, b, gs, bits, 1), seconds * 0.2)
+    xf = O.bf16_to_f32(x)
+    cm, em = timed(lambda: xf @ O.dequantize(w, s, b, gs, bits).T, seconds * 0.2, min_calls=2)
     return {
         "value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": f"{calls} calls of the same qmv shape (M=1 K=5120 N=17408 4-bit) in {el:.1f} s on {threads} "
-                  f"threads; 1 thread: {nbytes * c1 / e1 / 1e9:.3f} GB/s ({c1} calls)",
+                  f"threads; 1 thread: {nbytes * c1 / e1 / 1e9:.3f} GB/s ({c1} calls); dequantize-then-matmul: "
+                  f"{nbytes * cm / em / 1e9:.3f} GB/s ({cm} calls)",
         "us_per_call": round(el / calls * 1e6, 1),
+        "materialize": {"value": round(nbytes * cm / em / 1e9, 3), "unit": "GB/s",
+                        "us_per_call": round(em / cm * 1e6, 1), "calls": cm,
+                        "what": "single-threaded C dequantize of W to f32, then f32 x @ W^T in numpy"},
     }
 
 
