@@ -8,6 +8,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "kernels.h"
 #include <cstdlib>
@@ -30,6 +32,32 @@ int set_error(int code, const char* fmt, ...) {
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(LISAQ_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return LISAQ_OK;
+}
+
+int allow_dyn_lds(const void* fn, size_t bytes, const char* what) {
+  if (bytes <= 64 * 1024) return LISAQ_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(LISAQ_EHIP, "%s: no current device", what);
+  struct Entry {
+    int dev;
+    const void* fn;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> done;  // (device, kernel) pairs already raised, with their size
+  std::lock_guard<std::mutex> lock(mu);
+  for (Entry& en : done)
+    if (en.dev == dev && en.fn == fn) {
+      if (en.bytes >= bytes) return LISAQ_OK;
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+      if (e != hipSuccess) return set_error(LISAQ_EHIP, "%s: LDS %zu bytes: %s", what, bytes, hipGetErrorString(e));
+      en.bytes = bytes;
+      return LISAQ_OK;
+    }
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) return set_error(LISAQ_EHIP, "%s: LDS %zu bytes: %s", what, bytes, hipGetErrorString(e));
+  done.push_back(Entry{dev, fn, bytes});
   return LISAQ_OK;
 }
 

@@ -36,6 +36,10 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
 // Status plumbing shared by the C-ABI translation units.
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Lets kernel `fn` take `bytes` of dynamic LDS on the current device (above
+// the 64 KB default).  The attribute is set once per device and kernel (the
+// largest size asked for so far), not on every launch.
+int allow_dyn_lds(const void* fn, size_t bytes, const char* what);
 
 }  // namespace lisaq
 

@@ -126,11 +126,7 @@ __global__ __launch_bounds__(1024) void sort_kernel(const int32_t* __restrict__ 
 int launch_sort(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,
                 int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets) {
   const size_t lds = sizeof(int32_t) * (size_t)(E + 1 + 16 * E);
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return set_error(LISAQ_EHIP, "moe_sort: LDS %zu bytes: %s", lds, hipGetErrorString(e));
-  }
+  if (int rc = allow_dyn_lds((const void*)sort_kernel, lds, "moe_sort")) return rc;
   hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(1024), lds, st, ids, R, E, top_k, sorted_idx, order,
                      token_rows, inverse, offsets);
   return check_launch("moe_sort");
@@ -566,10 +562,7 @@ int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, i
   if (E > kTileTableMaxExperts)
     return set_error(LISAQ_EUNSUPPORTED, "gather_qmm: E=%d experts (at most %d)", E, kTileTableMaxExperts);
   const int lds = 2 * E * 4;
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)tile_table_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return set_error(LISAQ_EHIP, "gather_tile_table: LDS %d bytes: %s", lds, hipGetErrorString(e));
-  }
+  if (int rc = allow_dyn_lds((const void*)tile_table_kernel, lds, "gather_tile_table")) return rc;
   hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), lds, st, ids, offs, R, E, N, limit, VR, BM, BN,
                      qmv_tab, qmv_cap, qmm_tab, qmm_cap, counts);
   return check_launch("gather_tile_table");

@@ -156,10 +156,7 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
   int lds = 0;
   qmm_fn fn = split ? qmm_pick<true>(c, bits, gs, &lds) : qmm_pick<false>(c, bits, gs, &lds);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmm: LDS %d bytes: %s", lds, hipGetErrorString(e));
-  }
+  if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm")) return rc;
   LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
   p.ksplit = split ? c.S : 1;
   p.partial = split ? static_cast<float*>(ws) : nullptr;

@@ -497,10 +497,7 @@ int qmv16_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, 
 #ifdef LISAQ_EXPERIMENT
   if (const char* d = getenv("LISAQ_DEBUG")) p.debug = atoi(d);
 #endif
-  if (c.lds_bytes > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes);
-    if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmv16: LDS %d bytes: %s", c.lds_bytes, hipGetErrorString(e));
-  }
+  if (int rc = allow_dyn_lds((const void*)fn, c.lds_bytes, "qmv16")) return rc;
   hipLaunchKernelGGL(fn, dim3(grid_x), dim3(64 * c.NW), c.lds_bytes, stream, p);
   return check_launch("qmv16");
 }

@@ -419,10 +419,7 @@ int qmvd_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
   p.rpr = c.S;
   p.tile_rows = c.tile_rows;
   p.sbi = c.sbi;
-  if (c.lds_bytes > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes);
-    if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmvd: LDS %d bytes: %s", c.lds_bytes, hipGetErrorString(e));
-  }
+  if (int rc = allow_dyn_lds((const void*)fn, c.lds_bytes, "qmvd")) return rc;
   hipLaunchKernelGGL(fn, dim3(grid_x), dim3(T), c.lds_bytes, stream, p);
   return check_launch("qmvd");
 }

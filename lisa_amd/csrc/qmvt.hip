@@ -547,18 +547,11 @@ int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
 #ifdef LISAQ_EXPERIMENT
   if (const char* d = getenv("LISAQ_DEBUG")) p.debug = atoi(d);
 #endif
-  if (c.lds_bytes > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes);
-    if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmvt: LDS %d bytes: %s", c.lds_bytes, hipGetErrorString(e));
-  }
   // tile-table launches: one tile per block (the table gives each block its tile)
   const int tpb = p.tiles ? 1 : (c.tpb > 0 ? c.tpb : 1);
   int lds = c.lds_bytes;
   if (tpb != c.tpb) lds = qmvt_layout(c.slab_groups, gs, p.M, c.MQ, bits, c.NW * tpb, c.U).total;
-  if (lds > 64 * 1024 && lds != c.lds_bytes) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return set_error(LISAQ_EHIP, "qmvt: LDS %d bytes: %s", lds, hipGetErrorString(e));
-  }
+  if (int rc = allow_dyn_lds((const void*)fn, lds, "qmvt")) return rc;
   hipLaunchKernelGGL(fn, dim3((grid_x + tpb - 1) / tpb), dim3(64 * c.NW * tpb), lds, stream, p);
   return check_launch("qmvt");
 }
