@@ -153,11 +153,11 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
     const QmmConfig c1 = qmm_config(p.M, p.N, p.K, gs, bits, false);
     return qmm_launch(stream, c1, p, bits, gs, c1.grid, grid_y, nullptr, 0);
   }
+  LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
   int lds = 0;
   qmm_fn fn = split ? qmm_pick<true>(c, bits, gs, &lds) : qmm_pick<false>(c, bits, gs, &lds);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);
   if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm")) return rc;
-  LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
   p.ksplit = split ? c.S : 1;
   p.partial = split ? static_cast<float*>(ws) : nullptr;
   p.full_tiles = split ? c.full_tiles : 0;

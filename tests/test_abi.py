@@ -97,6 +97,11 @@ def test_empty_problem_is_a_no_op():
 
 def test_other_rejections():
     lib = _lib.load()
+    # x of 2^32 elements: refused before anything is enqueued
+    assert lib.lisaq_qmm(None, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, 256, 4096, 64, 4, None, 0) == _lib.EINVAL_SHAPE
+    assert b"2^31" in lib.lisaq_last_error()
+    assert lib.lisaq_quantized_matmul(None, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, 256, 4096, 1, 64, 4,
+                                      None, 0) == _lib.EINVAL_SHAPE
     assert lib.lisaq_qmv(None, FAKE, FAKE, FAKE, FAKE, FAKE, 33, 64, 128, 64, 4, None, 0) == _lib.EINVAL_SHAPE
     assert lib.lisaq_moe_route(None, FAKE, 4, 2000, 8, FAKE, FAKE) == _lib.EINVAL_SHAPE
     assert lib.lisaq_moe_route(None, FAKE, 4, 128, 0, FAKE, FAKE) == _lib.EINVAL_SHAPE
