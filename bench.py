@@ -35,8 +35,8 @@ METRIC = "4-bit qmv GB/s (% HBM peak) @M=1; qmm TFLOP/s (% bf16 MFMA peak) @M=20
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload, each
 # scaled by the counter's reading for a 64 MiB device copy (see the profiles/ summaries for the
 # commands and raw counts).
-QMV_TRAFFIC_BYTES = round((24587.8 * 1.9993 + 136.0) * 1024)
-QMM_TRAFFIC_BYTES = round((223968.6 * 1.9993 + 133388.0) * 1024)
+QMV_TRAFFIC_BYTES = round((24584.0 * 1.9993 + 136.0) * 1024)
+QMM_TRAFFIC_BYTES = round((223336.7 * 1.9993 + 133386.9) * 1024)
 QMV_KERNEL = "lisaq::qmvp_kernel<4, 64, 3, 2, 16, 1>"
 QMM_KERNEL = "lisaq::qmm_kernel<4, 64, 8, 1, 8, true>"  # M=2048: 256-row tiles, last round split over K (+ qmm_hybrid_reduce_kernel)
 
@@ -49,8 +49,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--qmm-steps", type=int, default=20)
+    ap.add_argument("--qmm-warmup", type=int, default=10)
     ap.add_argument("--sets", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -94,7 +95,7 @@ def main():
         return ops.quantized_matmul(x, w, s, b, True, gs, bits)
 
     with torch.cuda.stream(stream):
-        for i in range(max(args.warmup, len(sets))):  # eager warmup (also allocates the workspace)
+        for i in range(len(sets)):  # eager pass over every weight set (also allocates the workspace)
             step(i)
     stream.synchronize()
 
@@ -105,7 +106,8 @@ def main():
                 step(i)
         return g
 
-    g_warm = capture(len(sets))
+    # W untimed warm-up steps, replayed from a graph like the timed ones
+    g_warm = capture(max(args.warmup, 1))
     g_timed = capture(args.steps)
     with torch.cuda.stream(stream):
         g_warm.replay()
@@ -133,7 +135,7 @@ def main():
     wq = sets[0]
     xq = torch_x(Mq, K, device=dev, generator=gen)
     with torch.cuda.stream(stream):
-        for _ in range(3 if args.qmm_steps else 0):
+        for _ in range(args.qmm_warmup if args.qmm_steps else 0):
             ops.quantized_matmul(xq, *wq, True, gs, bits)
     torch.cuda.synchronize()
     q0 = torch.cuda.Event(enable_timing=True)
