@@ -196,9 +196,10 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def _time_graph(stream, fn, n_sets, steps):
+def _time_graph(stream, fn, n_sets, steps, warm_s=0.02):
     """Average seconds per call of fn(i) over `steps` calls replayed from a HIP graph (i cycles
-    over n_sets inputs), after one warm-up pass."""
+    over n_sets inputs), after untimed replays of the same graph for at least `warm_s` seconds
+    (steady clock; the first replays of a new graph over new buffers run slow)."""
     import torch
 
     with torch.cuda.stream(stream):
@@ -209,9 +210,13 @@ def _time_graph(stream, fn, n_sets, steps):
     with torch.cuda.graph(g, stream=stream):
         for i in range(steps):
             fn(i)
-    with torch.cuda.stream(stream):
-        g.replay()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reps = 0
+    while reps < 2 or time.perf_counter() - t0 < warm_s:
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
+        reps += 1
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
