@@ -328,7 +328,7 @@ def cpu_baseline(M, N, K, bits, gs, seconds):
     cm, em = timed(lambda: xf @ O.dequantize(w, s, b, gs, bits).T, seconds * 0.2, min_calls=2)
     return {
         "value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": f"{calls} calls of the same qmv shape (M=1 K=5120 N=17408 4-bit) in {el:.1f} s on {threads} "
+        "sample": f"{calls} calls of the same qmv shape (M={M} K={K} N={N} {bits}-bit) in {el:.1f} s on {threads} "
                   f"threads; 1 thread: {nbytes * c1 / e1 / 1e9:.3f} GB/s ({c1} calls); dequantize-then-matmul: "
                   f"{nbytes * cm / em / 1e9:.3f} GB/s ({cm} calls)",
         "us_per_call": round(el / calls * 1e6, 1),
