@@ -89,6 +89,10 @@ static int validate_mm(const char* op, const void* x, const uint32_t* w, const v
 static int run_qmv(hipStream_t st, const QmvConfig& c, const void* x, const uint32_t* w, const void* s,
                    const void* b, void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, void* ws,
                    size_t ws_bytes) {
+  // the streaming kernel's split over K is an option: without room for its
+  // parts it runs unsplit
+  if (c.kind == 2 && c.S > 1 && (ws == nullptr || ws_bytes < c.ws_bytes || !aligned(ws, 256)))
+    return run_qmv(st, qmv_config(M, N, K, gs, bits, true), x, w, s, b, y, M, N, K, gs, bits, nullptr, 0);
   if (c.S > 1) {
     LISAQ_REQUIRE(ws != nullptr && ws_bytes >= c.ws_bytes, LISAQ_EWORKSPACE,
                   "qmv: workspace of %zu bytes required (got %zu)", c.ws_bytes, ws_bytes);

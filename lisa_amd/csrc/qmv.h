@@ -60,7 +60,7 @@ QmvConfig qmv16_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
 int qmv16_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmv16_lds_bytes(int SG, int gs, int M, int MQ, int bits, int NW);
 bool qmvt_supported(int64_t M, int64_t K, int gs, int bits);
-QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool allow_split = true);
 int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmvt_lds_bytes(const QmvConfig& c, int gs, int M, int bits);
 bool qmvd_supported(int64_t M, int64_t N, int64_t K, int gs, int bits);

@@ -516,7 +516,7 @@ QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool sin
   }
   if (f != '3' && f != '1' && f != 't' && (M == 1 || f == 'd') && qmvd_supported(M, N, K, gs, bits))
     return qmvd_config(M, N, K, gs, bits);
-  if (f != '3' && f != '1' && qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits);
+  if (f != '3' && f != '1' && qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits, !single_pass);
   if (f != '3' && qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
   return qmv32_config(M, N, K, gs, bits, true);
 }

@@ -218,7 +218,10 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
   KConst kc;
   kc.init();
   const int nslab = (p.G + SG - 1) / SG;  // x slabs
-  for (int xsl = 0; xsl < nslab; ++xsl) {
+  // split over K (grid y = p.S, plain launches only): this workgroup's x slabs
+  const int sper = (nslab + p.S - 1) / p.S;
+  const int xs0 = (int)blockIdx.y * sper, xs1 = xs0 + sper < nslab ? xs0 + sper : nslab;
+  for (int xsl = xs0; xsl < xs1; ++xsl) {
     const int g_begin = xsl * SG;
     const int GL = (p.G - g_begin) < SG ? (p.G - g_begin) : SG;
     const int nws = GL / GPS;  // W slabs in this x slab
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
     for (int d = 0; d < D; ++d)
       if (d < mine) load_slab(d, ring[d], sring[d], bring[d]);
 
-    if (xsl > 0) __syncthreads();
+    if (xsl > xs0) __syncthreads();
     // x staging, part 2: permute to the unpack order, pre-scale, sum, write LDS
     {
       float* xs = reinterpret_cast<float*>(xs4);
@@ -444,8 +447,22 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
 #pragma unroll
     for (int ii = 0; ii < MR; ++ii) {
       const int m = 16 * a + 4 * q + ii;
-      if (m < M) y[(int64_t)m * p.N + n] = f2bf(yacc[a][ii]);
+      if (m >= M) continue;
+      if (p.S > 1)  // f32 part of split blockIdx.y, summed in split order by qmvt_split_reduce_kernel
+        p.partial[((int64_t)blockIdx.y * p.part_rows + m) * p.N + n] = yacc[a][ii];
+      else
+        y[(int64_t)m * p.N + n] = f2bf(yacc[a][ii]);
     }
+}
+
+// y = bf16(sum over the S parts of the f32 partials [S][M][N]), parts added in order.
+__global__ __launch_bounds__(256) void qmvt_split_reduce_kernel(const float* __restrict__ part,
+                                                                uint16_t* __restrict__ y, int64_t MN, int S) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= MN) return;
+  float v = part[i];
+  for (int s = 1; s < S; ++s) v += part[(int64_t)s * MN + i];
+  y[i] = f2bf(v);
 }
 
 // ---------------------------------------------------------------------------
@@ -464,7 +481,7 @@ bool qmvt_supported(int64_t M, int64_t K, int gs, int bits) {
          gs * bits >= 128 && pick_sb(K, gs, bits) != 0;
 }
 
-QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool allow_split) {
   QmvConfig c{};
   const int G = (int)(K / gs);
   const int SB = pick_sb(K, gs, bits);
@@ -487,8 +504,6 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   while (SG > GPS && SG * per_group > 40 * 1024) SG = (SG + 1) / 2;
   SG = ((SG + GPS - 1) / GPS) * GPS;
   if (SG > G) SG = G;
-  c.slab_groups = SG;
-  c.S_inner = (G + SG - 1) / SG;
   // two tiles per block when there are rows of x to share and tiles to spare
   // (measured: faster at N = 17408 with 2-4 rows of x; slower at N = 9728, no gain at 8 rows)
   c.tpb = (M >= 2 && M <= 4 && c.NW == 4 && c.tiles >= 1024) ? 2 : 1;
@@ -496,8 +511,34 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
     const int v = atoi(env);
     if (v == 1 || (v == 2 && c.NW <= 4)) c.tpb = v;
   }
+  // Fewer blocks than compute units (e.g. N = 2560: 160 row tiles): split K
+  // over S workgroups (grid y), each a whole number of x slabs, f32 parts in
+  // the workspace summed by a second launch.  Measured at 2560 x 9728: 2 rows
+  // of x 8.1 us unsplit (S = 2..4 slower), 4 rows 10.8 -> 9.6 us at S = 3,
+  // 8 rows 14.1 -> 12.4 us at S = 4 (S = 2 never the best).
+  c.S = 1;
+  if (allow_split && M >= 4) {
+    const int blocks = (c.tiles + c.tpb - 1) / c.tpb;
+    int S = blocks < 256 ? (M >= 8 ? 4 : 3) : 1;
+    if (const char* env = getenv("LISAQ_QMVT_SPLIT")) {  // tuning: parts (1 disables)
+      const int v = atoi(env);
+      if (v >= 1 && v <= 8) S = v;
+    }
+    if (S > 4) S = 4;
+    if (S > 1) {
+      int sg = (G + S - 1) / S;
+      sg = ((sg + GPS - 1) / GPS) * GPS;
+      if (sg < SG) SG = sg;
+      const int nslab = (G + SG - 1) / SG;
+      const int per = (nslab + S - 1) / S;
+      S = (nslab + per - 1) / per;  // every part non-empty
+    }
+    c.S = S;
+  }
+  c.slab_groups = SG;
+  c.S_inner = (G + SG - 1) / SG;
   c.lds_bytes = qmvt_layout(SG, gs, (int)M, c.MQ, bits, c.NW * c.tpb, SB).total;
-  c.ws_bytes = 0;
+  c.ws_bytes = c.S > 1 ? kQmvCounterBytes + (size_t)c.S * M * N * 4 : 0;
   c.kind = 2;
   c.tile_rows = 16;
   return c;
@@ -541,7 +582,7 @@ int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
   else if (bits == 2 && gs == 64) fn = pick_t<2, 64>(c.MQ, c.MR, c.U, c.NW);
   else if (bits == 2 && gs == 128) fn = pick_t<2, 128>(c.MQ, c.MR, c.U, c.NW);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmvt: bits=%d gs=%d MQ=%d SB=%d NW=%d", bits, gs, c.MQ, c.U, c.NW);
-  p.S = 1;
+  p.S = p.tiles ? 1 : c.S;
   p.S_inner = c.S_inner;
   p.slab_groups = c.slab_groups;
 #ifdef LISAQ_EXPERIMENT
@@ -552,8 +593,13 @@ int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
   int lds = c.lds_bytes;
   if (tpb != c.tpb) lds = qmvt_layout(c.slab_groups, gs, p.M, c.MQ, bits, c.NW * tpb, c.U).total;
   if (int rc = allow_dyn_lds((const void*)fn, lds, "qmvt")) return rc;
-  hipLaunchKernelGGL(fn, dim3((grid_x + tpb - 1) / tpb), dim3(64 * c.NW * tpb), lds, stream, p);
-  return check_launch("qmvt");
+  hipLaunchKernelGGL(fn, dim3((grid_x + tpb - 1) / tpb, p.S), dim3(64 * c.NW * tpb), lds, stream, p);
+  int rc = check_launch("qmvt");
+  if (rc || p.S == 1) return rc;
+  const int64_t MN = (int64_t)p.M * p.N;
+  hipLaunchKernelGGL(qmvt_split_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, stream,
+                     (const float*)p.partial, p.y, MN, p.S);
+  return check_launch("qmvt_split_reduce");
 }
 
 }  // namespace lisaq

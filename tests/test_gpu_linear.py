@@ -133,6 +133,37 @@ def test_qmm_prefill_shapes_sampled_rows(dev, oracle, M, N, K, bits):
     assert_close_bf16(got, ref, what=f"prefill M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M", [4, 8])
+def test_qmv_split_k_and_its_fallback(dev, oracle, M):
+    """Few row tiles (N = 2560): the streaming matvec splits K over workgroups when the workspace holds
+    the parts; given none, the same call runs unsplit. Both against the oracle, and close to each other."""
+    import torch
+
+    from lisa_amd import _lib
+
+    N, K, gs, bits = 2560, 9728, 64, 4
+    rng = np.random.default_rng(2560 + M)
+    w, s, b = np_linear(rng, N, K, bits, gs)
+    x = np_x(rng, M, K)
+    ref = oracle.qmv(x, w, s, b, gs, bits)
+    lib = _lib.load()
+    need = lib.lisaq_quantized_matmul_workspace(M, N, K, gs, bits)
+    assert need > 0  # the split is on for this shape
+    xd, wd, sd, bd = to_dev_bf16(x, dev), to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
+    outs = []
+    for with_ws in (True, False):
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        ws = ops.workspace(dev, need) if with_ws else None
+        _lib.call("lisaq_quantized_matmul", torch.cuda.current_stream().cuda_stream, xd.data_ptr(), wd.data_ptr(),
+                  sd.data_ptr(), bd.data_ptr(), y.data_ptr(), M, N, K, 1, gs, bits,
+                  ws.data_ptr() if with_ws else None, need if with_ws else 0)
+        got = from_dev_bf16(y)
+        assert_close_bf16(got, ref, what=f"qmv M={M} {'split' if with_ws else 'unsplit (no workspace)'}")
+        outs.append(bf16_bits_to_f32(got))
+    # same tolerance between the two as against the oracle (they differ in summation order only)
+    assert (np.abs(outs[0] - outs[1]) <= 2e-2 + 1e-2 * np.abs(outs[1])).all()
+
+
 @pytest.mark.parametrize("bits", [2, 4])
 def test_north_star_qmv_shape(dev, oracle, bits):
     rng = np.random.default_rng(17408 + bits)
