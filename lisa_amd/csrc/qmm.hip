@@ -84,10 +84,6 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool all
     }
   }
   c.WN = 8;
-  if (const char* env = getenv("LISAQ_QMM_MT")) {  // tuning: 4, 6, 8
-    const int v = atoi(env);
-    if (v == 4 || v == 6 || v == 8) c.MT = v;
-  }
   c.NT = 8 / c.WN;
   c.BM = 32 * c.MT;
   c.BN = 32 * c.NT * c.WN;
@@ -123,9 +119,12 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool all
     while (S > 1 && nk / S < 8) --S;
     c.S = S;
   }
+  // tuning: a split count for the per-part layout, honoured with 128-row
+  // tiles only -- the tile height the small-grid rule above always picks and
+  // the split tests cover (taller tiles with this layout are never dispatched)
   if (const char* env = getenv("LISAQ_QMM_SPLIT")) {
     const int v = atoi(env);
-    if (v >= 1 && v <= nk && allow_split) c.S = v;
+    if (v >= 1 && v <= nk && allow_split && c.MT == 4) c.S = v;
   }
   if (c.S > 1) {
     const int per = (nk + c.S - 1) / c.S;
