@@ -406,6 +406,9 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
             }
           }
           const float2 sbv = make_float2(sf[gl], bf[gl]);
+          // 4 bits: s*(acc - 128 sx) + b*sx = s*acc + (b - 128 s)*sx, the second
+          // factor once per group (2 bits: the scaled sum st differs from sx)
+          const float c128 = fmaf(-128.0f, sbv.x, sbv.y);
 #pragma unroll
           for (int a = 0; a < MQ; ++a) {
             const f32x4v sx = xs4[(g * MQ + a) * 4 + q];
@@ -413,8 +416,12 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
             if (BITS == 2) st = xs4[XT + (g * MQ + a) * 4 + q];
 #pragma unroll
             for (int ii = 0; ii < MR; ++ii) {  // rows 4q+ii >= M are never stored
-              const float t = acc[a][ii] - 128.0f * st[ii];
-              yacc[a][ii] = fmaf(sbv.x, t, fmaf(sbv.y, sx[ii], yacc[a][ii]));
+              if (BITS == 4) {
+                yacc[a][ii] = fmaf(sbv.x, acc[a][ii], fmaf(c128, sx[ii], yacc[a][ii]));
+              } else {
+                const float t = acc[a][ii] - 128.0f * st[ii];
+                yacc[a][ii] = fmaf(sbv.x, t, fmaf(sbv.y, sx[ii], yacc[a][ii]));
+              }
             }
           }
         }
