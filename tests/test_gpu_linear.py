@@ -159,6 +159,12 @@ def test_qmv_split_k_and_its_fallback(dev, oracle, M):
                   ws.data_ptr() if with_ws else None, need if with_ws else 0)
         got = from_dev_bf16(y)
         assert_close_bf16(got, ref, what=f"qmv M={M} {'split' if with_ws else 'unsplit (no workspace)'}")
+        if with_ws:  # parts summed in part order: the same bits on a repeat
+            y2 = torch.empty_like(y)
+            _lib.call("lisaq_quantized_matmul", torch.cuda.current_stream().cuda_stream, xd.data_ptr(),
+                      wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), y2.data_ptr(), M, N, K, 1, gs, bits,
+                      ws.data_ptr(), need)
+            assert np.array_equal(from_dev_bf16(y2), got)
         outs.append(bf16_bits_to_f32(got))
     # same tolerance between the two as against the oracle (they differ in summation order only)
     assert (np.abs(outs[0] - outs[1]) <= 2e-2 + 1e-2 * np.abs(outs[1])).all()
