@@ -491,8 +491,10 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
   L.g = take((size_t)R * I * 2);
   L.u = take((size_t)R * I * 2);
   L.d = take((size_t)R * H * 2);
-  const size_t g1 = lisaq_gather_qmm_workspace(R, I, H, E, gs, bits);
-  const size_t g2 = lisaq_gather_qmm_workspace(R, H, I, E, gs, bits);
+  // the tables exactly as lisaq_moe_forward lays them out: runs of at most T
+  // rows (a token picks an expert once)
+  const size_t g1 = gather_layout(R, I, H, E, gs, bits, T).total;
+  const size_t g2 = gather_layout(R, H, I, E, gs, bits, T).total;
   L.gws = take(g1 > g2 ? g1 : g2);
   L.total = o;
   return L;
