@@ -332,16 +332,24 @@ QmvConfig qmvd_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   const int C = (int)(K / 32);
   const int G = (int)(K / gs);
   c.MR = M == 1 ? 1 : 2;
-  // threads per workgroup: T = 64*NW >= C with the fewest idle lanes, T >= 256 preferred
+  // threads per workgroup: the smallest T = 64*NW >= C whose idle lanes
+  // (T - (T/C)*C) are at most 1/5 of T, else the fewest idle lanes.
+  // Measured (M = 1, 4-bit, cold): C = 80 (K = 2560): T = 192 (two rows side
+  // by side, 17% idle) 6.07 us, T = 256 6.21, T = 320 (no idle lane) 6.54;
+  // C = 128: T = 128 4.88 us, T = 256 5.13.
   int best = -1;
   double best_cost = 1e30;
   for (int nw = 1; nw <= kQmvdMaxThreads / 64; ++nw) {
     const int T = 64 * nw;
     if (T < C) continue;
     const int rpr = T / C;
-    const double cost = (double)(T - rpr * C) / T + (T < 256 ? 0.05 : 0.0);
-    if (cost < best_cost - 1e-9) {
-      best_cost = cost;
+    const double idle = (double)(T - rpr * C) / T;
+    if (idle <= 0.2) {
+      best = nw;
+      break;
+    }
+    if (idle < best_cost - 1e-9) {
+      best_cost = idle;
       best = nw;
     }
   }
@@ -352,9 +360,12 @@ QmvConfig qmvd_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   }
   const int T = 64 * c.NW;
   c.S = T / C;  // rows side by side
-  // rows per thread: the largest of 8/4/2 that still leaves >= 512 workgroups
-  int lpt = 8;
-  while (lpt > 2 && (N + (int64_t)c.S * lpt - 1) / ((int64_t)c.S * lpt) < 512) lpt /= 2;
+  // rows per thread: 4, or 2 when 4 leaves fewer than 256 workgroups.
+  // Measured (M = 1, 4-bit, cold): 5120 x 17408 LPT 4 (1280 workgroups)
+  // 19.1 us, 8 (640) 19.8, 2 (2560) 26.1; 2560 x 9728 LPT 4 7.50 us, 2 7.76,
+  // 8 8.6; 9728 x 2560 LPT 4 6.07 us, 2 6.89, 8 7.0.
+  int lpt = 4;
+  if ((N + (int64_t)c.S * lpt - 1) / ((int64_t)c.S * lpt) < 256) lpt = 2;
   if (const char* env = getenv("LISAQ_QMVD_LPT")) {
     const int v = atoi(env);
     if (v == 2 || v == 4 || v == 8 || v == 16) lpt = v;
