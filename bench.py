@@ -59,6 +59,8 @@ def main():
     ap.add_argument("--no-table", action="store_true", help="skip the per-configuration table")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run a plain 64 MiB device copy (the reference kernel for the HBM byte counters)")
+    ap.add_argument("--blaslt", action="store_true",
+                    help="only compare the prefill matmul with dequantize-then-hipBLASLt bf16 GEMM on the same shapes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
@@ -82,6 +84,9 @@ def main():
         return
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x5EED + 1)
+    if args.blaslt:
+        blaslt_compare(dev, gen)
+        return
     M, N, K, bits, gs = 1, 17408, 5120, 4, 64
 
     # --- qmv: cold-stream rotation over distinct weight sets ------------------
@@ -226,6 +231,35 @@ def _time_graph(stream, fn, n_sets, steps, warm_s=0.02):
     torch.cuda.synchronize()
     del g
     return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def blaslt_compare(dev, gen):
+    """The prefill matmul against the unfused alternative on the same inputs: W dequantized to
+    bf16 by lisaq_dequantize (bf16(s*q+b), the values the fused kernel feeds its matrix cores),
+    then torch.matmul (hipBLASLt) on the bf16 operands.  One JSON line per shape."""
+    import torch
+
+    from lisa_amd import ops
+    from lisa_amd.synth import torch_linear, torch_x
+
+    stream = torch.cuda.Stream()
+    for M, N, K in [(2048, 17408, 5120), (2048, 5120, 17408), (512, 17408, 5120), (128, 17408, 5120)]:
+        w, s, b = torch_linear(N, K, 4, 64, device=dev, generator=gen)
+        x = torch_x(M, K, device=dev, generator=gen)
+        wd = ops.dequantize(w, s, b, 64, 4)
+        fl = 2.0 * M * N * K
+        t_q = _time_graph(stream, lambda i: ops.quantized_matmul(x, w, s, b, True, 64, 4), 1, 10)
+        t_b = _time_graph(stream, lambda i: torch.matmul(x, wd.t()), 1, 10)
+        t_d = _time_graph(stream, lambda i: ops.dequantize(w, s, b, 64, 4), 1, 10)
+        y_q = ops.quantized_matmul(x, w, s, b, True, 64, 4).float()
+        y_b = torch.matmul(x, wd.t()).float()
+        print(json.dumps({"M": M, "N": N, "K": K, "fused_qmm_us": round(t_q * 1e6, 1),
+                          "fused_qmm_tflops": round(fl / t_q / 1e12, 1), "blaslt_bf16_us": round(t_b * 1e6, 1),
+                          "blaslt_bf16_tflops": round(fl / t_b / 1e12, 1), "dequantize_us": round(t_d * 1e6, 1),
+                          "dequantize_then_blaslt_tflops": round(fl / (t_b + t_d) / 1e12, 1),
+                          "max_abs_diff": (y_q - y_b).abs().max().item(),
+                          "max_abs_y": y_b.abs().max().item()}), flush=True)
+        del w, s, b, x, wd, y_q, y_b
 
 
 def config_table(dev, gen, stream):
