@@ -501,9 +501,11 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   c.tiles = (int)((N + 15) / 16);
   c.NW = 4;
   if (c.tiles * 4 < 2048 && nws >= 16) c.NW = 8;
-  if (const char* env = getenv("LISAQ_QMVT_NW")) {
+  if (const char* env = getenv("LISAQ_QMVT_NW")) {  // tuning: 4 or 8
+    // (2 waves per tile gave run-to-run differing bits in a sweep, cause not
+    // found: not offered)
     const int v = atoi(env);
-    if (v == 2 || v == 4 || v == 8) c.NW = v;
+    if (v == 4 || v == 8) c.NW = v;
   }
   // x slab: at most ~40 KB of staged x, a whole number of W slabs
   const int64_t per_group = (int64_t)gs * M * 2;
@@ -512,8 +514,9 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   SG = ((SG + GPS - 1) / GPS) * GPS;
   if (SG > G) SG = G;
   // two tiles per block when there are rows of x to share and tiles to spare
-  // (measured: faster at N = 17408 with 2-4 rows of x; slower at N = 9728, no gain at 8 rows)
-  c.tpb = (M >= 2 && M <= 4 && c.NW == 4 && c.tiles >= 1024) ? 2 : 1;
+  // (measured at N = 17408: 4 rows 23.3 -> 20.6 us, 8 rows 26.3 -> 25.4 us;
+  // slower at N = 9728)
+  c.tpb = (M >= 2 && M <= 8 && c.NW == 4 && c.tiles >= 1024) ? 2 : 1;
   if (const char* env = getenv("LISAQ_QMVT_TPB")) {  // tuning: 1 or 2
     const int v = atoi(env);
     if (v == 1 || (v == 2 && c.NW <= 4)) c.tpb = v;
@@ -562,7 +565,6 @@ static qmvt_fn pick_nw(int NW) {
   constexpr int D = (MQ == 1) ? (SB == 256 ? 2 : 3) : 2;
   if (NW == 4) return qmvt_kernel<BITS, GS, MQ, MR, SB, 4, D>;
   if (NW == 8) return qmvt_kernel<BITS, GS, MQ, MR, SB, 8, D>;
-  if (NW == 2) return qmvt_kernel<BITS, GS, MQ, MR, SB, 2, D + 2>;
   return nullptr;
 }
 

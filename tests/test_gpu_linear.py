@@ -175,11 +175,12 @@ def test_north_star_qmv_shape(dev, oracle, bits):
     rng = np.random.default_rng(17408 + bits)
     N, K = 17408, 5120
     w, s, b = np_linear(rng, N, K, bits, 64, s_std=0.02 if bits == 4 else 0.05, b_std=0.01 if bits == 4 else 0.02)
-    for M in (1, 8):
+    for M in (1, 5, 8):  # 5 and 8: two 16-row tiles per workgroup share the staged x
         x = np_x(rng, M, K)
         ref = oracle.qmv(x, w, s, b, 64, bits)
         got = _run(ops.quantized_matmul, dev, x, w, s, b, 64, bits)
         assert_close_bf16(got, ref, what=f"north-star qmv M={M} bits={bits}")
+        assert np.array_equal(_run(ops.quantized_matmul, dev, x, w, s, b, 64, bits), got)
 
 
 @pytest.mark.parametrize("bits", [2, 4])
