@@ -97,6 +97,19 @@ LISAQ_API int lisaq_qmm(void* stream, const void* x, const uint32_t* w, const vo
  * the split partials of jit::affine_qmm_splitk (JM:1885-1979) are f32 here. */
 LISAQ_API size_t lisaq_qmm_workspace(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 
+/* ---- residual add + RMSNorm, then the decode matvec ----------------------
+ * sum_out = bf16(x + r); normed = bf16(norm_w * bf16(sum_out * inv)),
+ * inv = 1/sqrt(mean(sum_out^2) + eps) (f32); y = quantized_matmul(normed).
+ * norm_out [M,K] receives normed (the matvec's input; caller-owned).
+ * Replaces jit::affine_qmv_fast_addnorm (JM:315-443, kernel
+ * norm_qmv.metal:293-423) with its eligibility: gs 64, 4 bits, M == 1,
+ * K > 4096, K % 512 == 0, N % 8 == 0 (else LISAQ_EUNSUPPORTED).  The
+ * workspace is lisaq_quantized_matmul_workspace(1, N, K, 64, 4) bytes. */
+LISAQ_API int lisaq_qmv_addnorm(void* stream, const void* x, const void* r, const void* norm_w,
+              const uint32_t* w, const void* scales, const void* biases, void* sum_out,
+              void* norm_out, void* y, int64_t M, int64_t N, int64_t K, float eps,
+              int group_size, int bits, void* workspace, size_t workspace_bytes);
+
 /* ---- dequantize / quantize ----------------------------------------------
  * out[rows,K] (bf16) = scales*code + biases.  Replaces ops::dequantize
  * (AO:37-84; GPU kernel jit::affine_dequantize JM:1316-1402). */

@@ -51,6 +51,8 @@ SIGNATURES = {
     "lisaq_qmm": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, vp, sz]),
     "lisaq_dequantize": (ci, [vp, vp, vp, vp, vp, i64, i64, ci, ci]),
     "lisaq_quantize": (ci, [vp, vp, ci, vp, vp, vp, i64, i64, ci, ci]),
+    "lisaq_qmv_addnorm": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_float,
+                               ci, ci, vp, sz]),
     "lisaq_moe_route": (ci, [vp, vp, i64, ci, ci, vp, vp]),
     "lisaq_moe_sort": (ci, [vp, vp, i64, ci, ci, vp, vp, vp, vp, vp]),
     "lisaq_gather_rows": (ci, [vp, vp, vp, vp, i64, i64]),

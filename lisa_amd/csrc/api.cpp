@@ -376,6 +376,27 @@ int lisaq_dequantize(void* stream, const uint32_t* w, const void* s, const void*
                            K, gs, bits);
 }
 
+int lisaq_qmv_addnorm(void* stream, const void* x, const void* r, const void* norm_w, const uint32_t* w,
+                      const void* s, const void* b, void* sum_out, void* norm_out, void* y, int64_t M, int64_t N,
+                      int64_t K, float eps, int gs, int bits, void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  // the reference's eligibility (JM:328-347): 4-bit, group 64, one row, K > 4096, qmv_fast shapes
+  LISAQ_REQUIRE(gs == 64 && bits == 4, LISAQ_EUNSUPPORTED, "qmv_addnorm: only gs64/b4 (got gs=%d bits=%d)", gs, bits);
+  LISAQ_REQUIRE(M == 1, LISAQ_EUNSUPPORTED, "qmv_addnorm: decode GEMV only (M=1), got M=%lld", (long long)M);
+  LISAQ_REQUIRE(N > 0 && K > 4096 && K % 512 == 0 && N % 8 == 0, LISAQ_EUNSUPPORTED,
+                "qmv_addnorm: shape ineligible (k=%lld, n=%lld)", (long long)K, (long long)N);
+  LISAQ_REQUIRE(x && r && norm_w && w && s && b && sum_out && norm_out && y, LISAQ_EINVAL_LAYOUT,
+                "qmv_addnorm: null tensor pointer");
+  LISAQ_REQUIRE(aligned(x, 16) && aligned(r, 16) && aligned(norm_w, 16) && aligned(sum_out, 16) &&
+                    aligned(norm_out, 16),
+                LISAQ_EINVAL_LAYOUT, "qmv_addnorm: x, r, norm weight, sum and norm rows must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (int rc = launch_add_rms(st, (const uint16_t*)x, (const uint16_t*)r, (const uint16_t*)norm_w,
+                              (uint16_t*)sum_out, (uint16_t*)norm_out, M, K, eps))
+    return rc;
+  return run_qmv(st, qmv_config(M, N, K, gs, bits), norm_out, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
+}
+
 int lisaq_quantize(void* stream, const void* w, int dtype, uint32_t* wq, void* s, void* b, int64_t rows,
                    int64_t K, int gs, int bits) {
   g_err[0] = 0;

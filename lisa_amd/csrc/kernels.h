@@ -14,6 +14,9 @@ int launch_sort(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k,
                 int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets);
 int launch_gather_rows(hipStream_t st, const uint16_t* x, const int32_t* rows, uint16_t* out,
                        int64_t R, int64_t H);
+// residual add + RMSNorm of M rows (addnorm.hip)
+int launch_add_rms(hipStream_t st, const uint16_t* x, const uint16_t* r, const uint16_t* nw, uint16_t* sum_out,
+                   uint16_t* norm_out, int64_t M, int64_t K, float eps);
 int launch_swiglu(hipStream_t st, const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n);
 int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const int32_t* inv,
                    uint16_t* out, int64_t T, int k, int64_t H);

@@ -176,6 +176,35 @@ def gather_qmm(x, w, scales, biases=None, lhs_indices=None, rhs_indices=None, tr
     return y
 
 
+def qmv_addnorm(x, r, norm_weight, w, scales, biases, eps: float, group_size=64, bits=4, write_norm=True):
+    """``jit::affine_qmv_fast_addnorm`` (matmul.rs:315-443): residual add + RMSNorm of x [1, K], then the
+    decode matvec on the normed row.  Returns ``(y [1, N], sum [1, K], normed [1, K] or None)`` like the
+    reference; ``write_norm`` only decides whether ``normed`` is returned."""
+    x = _bf16(x, "x")
+    r = _bf16(r, "r")
+    norm_weight = _bf16(norm_weight, "norm_weight")
+    w = _u32(w, "w")
+    scales = _bf16(scales, "scales")
+    biases = _bf16(biases, "biases")
+    _require(x.dim() == 2 and r.shape == x.shape, _lib.EINVAL_SHAPE, f"qmv_addnorm: x {tuple(x.shape)}, r {tuple(r.shape)}")
+    M, K = x.shape
+    N = w.shape[0]
+    _require(norm_weight.numel() == K, _lib.EINVAL_SHAPE, f"qmv_addnorm: norm weight of {norm_weight.numel()} != K={K}")
+    _require(w.dim() == 2 and w.shape[1] * 32 // bits == K, _lib.EINVAL_SHAPE,
+             f"qmv_addnorm: w {tuple(w.shape)} does not match K={K}, bits={bits}")
+    _require(scales.shape == (N, K // group_size) and biases.shape == scales.shape, _lib.EINVAL_SHAPE,
+             f"qmv_addnorm: scales/biases {tuple(scales.shape)} != ({N}, {K // group_size})")
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    sum_out = torch.empty_like(x)
+    norm_out = torch.empty_like(x)
+    lib = _lib.load()
+    ws = workspace(x.device, lib.lisaq_quantized_matmul_workspace(M, N, K, group_size, bits))
+    _lib.call("lisaq_qmv_addnorm", _stream(x), x.data_ptr(), r.data_ptr(), norm_weight.data_ptr(), w.data_ptr(),
+              scales.data_ptr(), biases.data_ptr(), sum_out.data_ptr(), norm_out.data_ptr(), y.data_ptr(), M, N, K,
+              float(eps), group_size, bits, ws.data_ptr(), ws.numel())
+    return y, sum_out, (norm_out if write_norm else None)
+
+
 def dequantize(w, scales, biases, group_size=64, bits=4):
     """``ops::dequantize`` (array_ops.rs:37-84): bf16 ``[..., K]``."""
     w = _u32(w, "w")

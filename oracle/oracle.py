@@ -137,6 +137,23 @@ def qmv_threads(x, w, scales, biases, group_size: int, bits: int, nthreads: int)
     return y
 
 
+def add_rms_norm(x, r, norm_w, eps: float):
+    """Prologue of affine_qmv_fast_addnorm (norm_qmv.metal:376-400): s = bf16(x + r);
+    inv = 1/sqrt(sum(s^2)/K + eps) in f32; normed = bf16(norm_w * bf16(s * inv)).  x, r: bf16 bits
+    [M, K]; norm_w: bf16 bits [K].  Returns (s, normed) as bf16 bits.  The sum of squares is taken
+    in float64 (the reference's order is Apple's simd_sum tree, not reproducible here)."""
+    x = _c(x, np.uint16)
+    r = _c(r, np.uint16)
+    K = x.shape[-1]
+    s = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(r))
+    sf = bf16_to_f32(s).astype(np.float32)
+    ss = (sf.astype(np.float64) ** 2).sum(axis=-1, keepdims=True).astype(np.float32)
+    inv = (np.float32(1.0) / np.sqrt(ss / np.float32(K) + np.float32(eps))).astype(np.float32)
+    t = bf16_to_f32(f32_to_bf16(sf * inv)).astype(np.float32)
+    normed = f32_to_bf16(bf16_to_f32(_c(norm_w, np.uint16)).reshape(1, K).astype(np.float32) * t)
+    return s, normed
+
+
 def topk_route(logits, k: int):
     lg = _c(logits, np.float32)
     T, E = lg.shape

@@ -115,6 +115,19 @@ def test_other_rejections():
                                 None, 0) == _lib.EWORKSPACE
 
 
+def test_qmv_addnorm_rejections():
+    """jit::affine_qmv_fast_addnorm's eligibility (matmul.rs:328-347), checked before anything is enqueued."""
+    lib = _lib.load()
+    call = lambda M, N, K, gs, bits, ptr=FAKE: lib.lisaq_qmv_addnorm(
+        None, ptr, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, M, N, K, 1e-6, gs, bits, None, 0)
+    assert call(1, 512, 5120, 32, 4) == _lib.EUNSUPPORTED
+    assert call(1, 512, 5120, 64, 2) == _lib.EUNSUPPORTED
+    assert call(2, 512, 5120, 64, 4) == _lib.EUNSUPPORTED and b"M=1" in lib.lisaq_last_error()
+    assert call(1, 512, 4096, 64, 4) == _lib.EUNSUPPORTED and b"ineligible" in lib.lisaq_last_error()
+    assert call(1, 500, 5120, 64, 4) == _lib.EUNSUPPORTED
+    assert call(1, 512, 5120, 64, 4, None) == _lib.EINVAL_LAYOUT
+
+
 def test_workspace_queries():
     lib = _lib.load()
     # one row: no workspace; a few rows over few row tiles (N = 2560: 160 tiles of 16 rows): the

@@ -268,3 +268,35 @@ def test_rejections_raise(dev):
     with pytest.raises(ops.LisaqError, match="dtype"):
         ops.quantized_matmul(torch.zeros(1, 128, device=dev), to_dev_u32(w, dev), to_dev_bf16(s, dev),
                              to_dev_bf16(b, dev))
+
+
+@pytest.mark.parametrize("N,K", [(264, 5120), (1000, 9728)])
+def test_qmv_addnorm(dev, oracle, N, K):
+    """Residual add + RMSNorm + matvec (jit::affine_qmv_fast_addnorm, matmul.rs:315-443): the sum row
+    bit-exact; the normed row within one bf16 step of the oracle (the f32 sum of squares may differ in
+    its last bit from the float64 one); y bitwise equal to the matvec on the kernel's own normed row and
+    within tolerance of the oracle's matvec on the oracle's normed row."""
+    import torch
+
+    rng = np.random.default_rng(N + K)
+    w, s, b = np_linear(rng, N, K, 4, 64)
+    x = np_x(rng, 1, K)
+    r = np_x(rng, 1, K)
+    from lisa_amd.synth import f32_to_bf16_bits
+    nw = f32_to_bf16_bits((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    dw = (to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev))
+    y, sm, nm = ops.qmv_addnorm(to_dev_bf16(x, dev), to_dev_bf16(r, dev), to_dev_bf16(nw, dev), *dw, 1e-6)
+    torch.cuda.synchronize()
+    s_ref, n_ref = oracle.add_rms_norm(x, r, nw, 1e-6)
+    assert np.array_equal(from_dev_bf16(sm), s_ref)
+    got_n = bf16_bits_to_f32(from_dev_bf16(nm))
+    ref_n = bf16_bits_to_f32(n_ref)
+    step = np.abs(ref_n) * 2.0**-7 + 1e-30
+    assert (np.abs(got_n - ref_n) <= step).all()
+    assert (got_n != ref_n).mean() < 0.01
+    chain = from_dev_bf16(ops.quantized_matmul(nm, *dw, True, 64, 4))
+    assert np.array_equal(from_dev_bf16(y), chain)
+    assert_close_bf16(from_dev_bf16(y), oracle.qmv(n_ref, w, s, b, 64, 4), what=f"qmv_addnorm N={N} K={K}")
+    _, _, none = ops.qmv_addnorm(to_dev_bf16(x, dev), to_dev_bf16(r, dev), to_dev_bf16(nw, dev), *dw, 1e-6,
+                                 write_norm=False)
+    assert none is None

@@ -243,3 +243,31 @@ def test_qmv_threads_matches_single(oracle):
     w, s, b = np_linear(rng, N, K)
     x = np_x(rng, 2, K)
     assert np.array_equal(oracle.qmv_threads(x, w, s, b, 64, 4, 7), oracle.qmv(x, w, s, b, 64, 4))
+
+
+def test_add_rms_norm_known_answer(oracle):
+    """norm_qmv.metal:383-400 by hand: s alternating 3, 4 (mean square 12.5, eps 0), norm weight 1.5.
+    3/sqrt(12.5) = 0.84853 rounds to bf16 0.84765625, times 1.5 = 1.271484375 -> 1.2734375;
+    4/sqrt(12.5) = 1.13137 rounds to 1.1328125, times 1.5 = 1.69921875, a tie -> 1.703125 (even).
+    Without the inner rounding the 4 would give 1.6953125: the double rounding is pinned."""
+    K = 8
+    x = f32_to_bf16_bits(np.array([[1, 3] * (K // 2)], np.float32))
+    r = f32_to_bf16_bits(np.array([[2, 1] * (K // 2)], np.float32))
+    nw = f32_to_bf16_bits(np.full(K, 1.5, np.float32))
+    s, normed = oracle.add_rms_norm(x, r, nw, 0.0)
+    assert np.array_equal(bf16_bits_to_f32(s), np.array([[3, 4] * (K // 2)], np.float32))
+    assert np.array_equal(bf16_bits_to_f32(normed), np.array([[1.2734375, 1.703125] * (K // 2)], np.float32))
+    # eps enters the mean: a zero row gives zeros, not NaN
+    s0, n0 = oracle.add_rms_norm(np.zeros((1, K), np.uint16), np.zeros((1, K), np.uint16), nw, 1e-6)
+    assert not np.isnan(bf16_bits_to_f32(n0)).any() and (bf16_bits_to_f32(n0) == 0).all()
+
+
+def test_add_rms_norm_unit_rms(oracle):
+    """With unit norm weight the normed row has mean square ~1 (float64 check of the formula's scale)."""
+    rng = np.random.default_rng(4)
+    x = np_x(rng, 3, 6144)
+    r = np_x(rng, 3, 6144)
+    nw = f32_to_bf16_bits(np.ones(6144, np.float32))
+    _, normed = oracle.add_rms_norm(x, r, nw, 1e-6)
+    ms = (bf16_bits_to_f32(normed).astype(np.float64) ** 2).mean(axis=-1)
+    assert np.allclose(ms, 1.0, atol=1e-2)
