@@ -61,6 +61,8 @@ def main():
                     help="only run a plain 64 MiB device copy (the reference kernel for the HBM byte counters)")
     ap.add_argument("--blaslt", action="store_true",
                     help="only compare the prefill matmul with dequantize-then-hipBLASLt bf16 GEMM on the same shapes")
+    ap.add_argument("--addnorm", action="store_true",
+                    help="only time the residual add + RMSNorm matvec against the plain matvec at the north-star shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
@@ -86,6 +88,9 @@ def main():
     gen.manual_seed(0x5EED + 1)
     if args.blaslt:
         blaslt_compare(dev, gen)
+        return
+    if args.addnorm:
+        addnorm_compare(dev, gen)
         return
     M, N, K, bits, gs = 1, 17408, 5120, 4, 64
 
@@ -231,6 +236,26 @@ def _time_graph(stream, fn, n_sets, steps, warm_s=0.02):
     torch.cuda.synchronize()
     del g
     return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def addnorm_compare(dev, gen):
+    """lisaq_qmv_addnorm (add + RMSNorm launch, then the matvec) against the plain matvec, 4-bit M=1
+    K=5120 N=17408, 8 rotating weight sets, graph-replayed.  One JSON line."""
+    import torch
+
+    from lisa_amd import ops
+    from lisa_amd.synth import torch_linear, torch_x
+
+    N, K, n_sets = 17408, 5120, 8
+    stream = torch.cuda.Stream()
+    sets = [torch_linear(N, K, 4, 64, device=dev, generator=gen) for _ in range(n_sets)]
+    x = torch_x(1, K, device=dev, generator=gen)
+    r = torch_x(1, K, device=dev, generator=gen)
+    nw = torch.ones(K, dtype=torch.bfloat16, device=dev)
+    t_q = _time_graph(stream, lambda i: ops.quantized_matmul(x, *sets[i % n_sets], True, 64, 4), n_sets, 400)
+    t_a = _time_graph(stream, lambda i: ops.qmv_addnorm(x, r, nw, *sets[i % n_sets], 1e-6), n_sets, 400)
+    print(json.dumps({"workload": "qmv 4-bit gs64 M=1 K=5120 N=17408", "qmv_us": round(t_q * 1e6, 2),
+                      "addnorm_qmv_us": round(t_a * 1e6, 2)}), flush=True)
 
 
 def blaslt_compare(dev, gen):
