@@ -29,6 +29,25 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
+int tune_int(const char* name, int dflt) {
+#ifdef LISAQ_TUNING
+  if (const char* v = getenv(name)) return atoi(v);
+#else
+  (void)name;
+#endif
+  return dflt;
+}
+
+int path_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : dflt;
+}
+
+char path_char(const char* name) {
+  const char* v = getenv(name);
+  return v ? v[0] : 0;
+}
+
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(LISAQ_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -104,8 +123,7 @@ static int run_qmv(hipStream_t st, const QmvConfig& c, const void* x, const uint
   p.s = (const uint16_t*)s;
   p.b = (const uint16_t*)b;
   p.y = (uint16_t*)y;
-  p.counters = (uint32_t*)ws;
-  p.partial = ws ? (float*)((char*)ws + kQmvCounterBytes) : nullptr;
+  p.partial = (float*)ws;
   p.tiles = nullptr;
   p.M = (int)M;
   p.N = (int)N;
@@ -322,6 +340,21 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
   // The M=1 schedule (same slabs, same waves) applied to every row gives each
   // row the arithmetic of an independent M=1 call.
   const QmvConfig c = qmv_config(1, N, K, gs, bits);
+  if (c.kind == 5) {
+    // one weight stream for all rows; every row's arithmetic is the one-row
+    // kernel's (the row split of the matrix cores never mixes rows of x)
+    const QmvConfig cw = qmv_config(M, N, K, gs, bits);
+    if (cw.kind == 5)
+      return run_qmv((hipStream_t)stream, cw, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
+    // staged x too large for all rows at once: two halves, each bitwise the same per row
+    const int64_t h = (M + 1) / 2;
+    const QmvConfig c1 = qmv_config(h, N, K, gs, bits), c2 = qmv_config(M - h, N, K, gs, bits);
+    if (c1.kind != 5 || c2.kind != 5) return set_error(LISAQ_EUNSUPPORTED, "serial_rows: no one-stream configuration");
+    rc = run_qmv((hipStream_t)stream, c1, x, w, s, b, y, h, N, K, gs, bits, ws, ws_bytes);
+    if (rc) return rc;
+    return run_qmv((hipStream_t)stream, c2, (const uint16_t*)x + h * K, w, s, b, (uint16_t*)y + h * N, M - h, N, K,
+                   gs, bits, ws, ws_bytes);
+  }
   if (c.kind == 4) {
     // the persistent kernel computes each of its (one or two) rows with the
     // one-row arithmetic, so pairs of rows share one pass over W
@@ -349,7 +382,7 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
   QmvConfig cm = c;
   cm.MR = M == 1 ? 1 : (M == 2 ? 2 : 4);  // accumulator rows in use; per-row arithmetic unchanged
   cm.lds_bytes = qmv_lds_bytes_for(c, gs, (int)M, bits);
-  cm.ws_bytes = c.S > 1 ? kQmvCounterBytes + (size_t)c.S * M * N * 4 : 0;
+  cm.ws_bytes = 0;  // one-row configurations never split K
   if (cm.lds_bytes <= 64 * 1024)
     return run_qmv((hipStream_t)stream, cm, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
   for (int64_t r = 0; r < M; ++r) {
@@ -557,8 +590,7 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   int rc;
   // Few tokens (T <= 8, the reference's decode window): fused path, two
   // launches, the first one routing (LISAQ_MOE_FUSED=0 selects the generic path)
-  const char* fenv = getenv("LISAQ_MOE_FUSED");
-  if (!(fenv && fenv[0] == '0') && moe_decode_supported(T, H, I, E, k, gs, bits)) {
+  if (path_int("LISAQ_MOE_FUSED", 1) != 0 && moe_decode_supported(T, H, I, E, k, gs, bits)) {
     if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, out, R, H, I, 1, gs, bits))) return rc;

@@ -33,6 +33,17 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Launch-geometry overrides for tuning runs.  Only a library built with
+// -DLISAQ_TUNING reads them (from the environment); the shipped library
+// always uses `dflt`.
+int tune_int(const char* name, int dflt);
+// Path selection among kernels that are each validated for the shape they
+// accept (the tests force every matvec kernel, the generic MoE path and the
+// matmul split counts this way).  Read in every build; unset means the
+// dispatcher's choice.
+int path_int(const char* name, int dflt);
+char path_char(const char* name);
+
 // Status plumbing shared by the C-ABI translation units.
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);

@@ -76,9 +76,8 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool all
   const int nk = (int)(K / 64);
   bool hybrid = false;
   {
-    const char* env = getenv("LISAQ_QMM_HYBRID");  // tuning: 0 disables
     const int64_t t8 = ((N + 255) / 256) * ((M + 255) / 256);
-    if (allow_split && !(env && env[0] == '0') && t8 >= 256 && t8 % 256 != 0 && nk >= 16) {
+    if (allow_split && tune_int("LISAQ_QMM_HYBRID", 1) && t8 >= 256 && t8 % 256 != 0 && nk >= 16) {
       c.MT = 8;
       hybrid = true;
     }
@@ -119,11 +118,11 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool all
     while (S > 1 && nk / S < 8) --S;
     c.S = S;
   }
-  // tuning: a split count for the per-part layout, honoured with 128-row
-  // tiles only -- the tile height the small-grid rule above always picks and
-  // the split tests cover (taller tiles with this layout are never dispatched)
-  if (const char* env = getenv("LISAQ_QMM_SPLIT")) {
-    const int v = atoi(env);
+  // path selection (tests): a split count for the per-part layout, honoured
+  // with 128-row tiles only -- the tile height the small-grid rule above
+  // always picks and the split tests cover
+  {
+    const int v = path_int("LISAQ_QMM_SPLIT", 0);
     if (v >= 1 && v <= nk && allow_split && c.MT == 4) c.S = v;
   }
   if (c.S > 1) {

@@ -11,36 +11,32 @@ struct QmvParams {
   const uint16_t* b;     // [(E,) N, G] bf16
   uint16_t* y;           // [rows, N] bf16
   float* partial;        // [S, part_rows, N] f32 (split-K only)
-  uint32_t* counters;    // [grid_x] arrival counters (split-K only), zero at rest
   const int4* tiles;     // gather: {expert, row start, rows, n tile} per block, or null
   int M;                 // rows (max rows per tile for gather)
   int N, K, G;           // G = K / group_size
   int part_rows;         // rows of the partial buffer
   int S, S_inner;        // slabs across workgroups (grid y) / walked inside one
   int slab_groups;       // groups per slab
-  int debug;             // experiment builds only: phases to skip
+  int debug;             // tuning builds only: phases to skip
   int chunks, rpr, tile_rows;  // dot kernel: 32-code chunks per row, rows side by side, rows per tile
   int sbi;               // dot kernel: 4-element scale/bias staging loads per thread
   // filled by qmv_launch from the config
 };
 
-// Split-K workspace: arrival counters live in a fixed region at the start
-// (one u32 per row tile, at most kQmvMaxTiles tiles) so that partials of any
-// launch geometry never overwrite another geometry's counters.
-constexpr int kQmvMaxTiles = 32768;
-constexpr size_t kQmvCounterBytes = (size_t)kQmvMaxTiles * 4;
 
 struct QmvConfig {
   int kind;       // 0: 32-row tiles (mfma 32x32x16), 1: 16-row tiles, 2: streaming 16-row tiles,
                   // 3: VALU dot kernel (U = rows per thread, S = rows side by side, S_inner = chunks),
-                  // 4: persistent one-row dot kernel (U = passes, S = ring depth, S_inner = chunks)
+                  // 4: persistent one-row dot kernel (U = passes, S = ring depth, S_inner = chunks),
+                  // 5: one-stream 1..8-row MFMA kernel (MR = staged rows, S = workgroups, U = ring units,
+                  //    tile_rows = 16-row tiles per workgroup at most)
   int tile_rows;  // rows of W per workgroup (32 or 16)
   int U, MQ, NW, S, S_inner, slab_groups, tiles, lds_bytes;
   int tpb;  // streaming kernel: 16-row tiles per block (0 or 1: one)
   int MR;         // streaming kernel: accumulator rows per lane group in use (1, 2 or 4)
   int sbi;        // dot kernel: scale/bias staging loads per thread
   int sbw;        // one-row kernel: bytes per lane of the scale/bias row loads
-  size_t ws_bytes;       // kQmvCounterBytes + partials (0 when S == 1)
+  size_t ws_bytes;       // f32 partials of a split over K (0 when S == 1)
 };
 
 // Launch geometry for M rows (1..32) of an [N, K] matrix.  With
@@ -52,7 +48,7 @@ QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool sin
 int qmv_lds_bytes_for(const QmvConfig& c, int gs, int M, int bits);
 
 // Kernel-specific halves (qmv.hip: 32-row tiles, qmv16.hip: 16-row tiles).
-QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass);
+QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
 int qmv32_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmv32_lds_bytes(int slab_groups, int gs, int M, int MQ, int bits, int NW);
 bool qmv16_supported(int64_t M, int gs, int bits);
@@ -68,6 +64,11 @@ QmvConfig qmvd_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
 int qmvd_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmvd_lds_bytes(const QmvConfig& c, int M);
 QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+// one-stream kernel for 1..8 rows (every row bitwise equal to a one-row call)
+constexpr int64_t kQmvwMaxBytes = 0x40000000;  // buffer ranges must stay below this
+QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
+bool qmvw_supported(int64_t M, int64_t N, int64_t K, int gs, int bits);
+int qmvw_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmvp_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 
 // Enqueue; grid_x = number of row tiles (or tile-table entries).

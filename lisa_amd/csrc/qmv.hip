@@ -22,14 +22,11 @@
 //    the hot loop.  For 2-bit codes three codes per 16-bit half are taken
 //    with masks only (values 128 + {1,4,16}*q) and x is pre-scaled by
 //    {1, 1/4, 1/16} (exact powers of two).
-//  * Split-K: the waves of a workgroup split the groups of one K slab; a row
-//    tile may be split over S slabs (blockIdx.y).  Slab partials (f32) go to
-//    the workspace and the last-arriving workgroup of the tile (per-tile
-//    counter) sums them in slab order, so results are deterministic.
+//  * The waves of a workgroup split the groups of one K slab; the workgroup
+//    walks the slabs of K one after the other (x re-staged per slab).
 #include "lisaq_common.h"
 #include "qmv.h"
 
-#include <cstdio>
 #include <cstdlib>
 
 namespace lisaq {
@@ -180,7 +177,6 @@ __global__ __launch_bounds__(512) void qmv_kernel(QmvParams p) {
   uint16_t* y = p.y;
   int n0 = tile * 32;
   int M = p.M;          // rows of x handled by this tile
-  int64_t row0 = 0;     // first x / y row of the tile
   if (p.tiles) {
     // gather: p.tiles[tile] = {expert, x row start, rows, n tile}
     const int4 t = p.tiles[tile];
@@ -191,7 +187,6 @@ __global__ __launch_bounds__(512) void qmv_kernel(QmvParams p) {
     bi += e * (int64_t)p.N * p.G;
     x += (int64_t)t.y * p.K;
     y += (int64_t)t.y * p.N;
-    row0 = t.y;
     M = t.z;
     n0 = t.w * 32;
   }
@@ -383,52 +378,15 @@ __global__ __launch_bounds__(512) void qmv_kernel(QmvParams p) {
   }
   if (wave != 0) return;
 
-  if (p.S == 1) {
-    if (n < p.N) {
-#pragma unroll
-      for (int q = 0; q < MQ; ++q)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 8 * q + 4 * h + i;
-          if (m < M) y[(int64_t)m * p.N + n] = f2bf(yacc[q][i]);
-        }
-    }
-    return;
-  }
-
-  // --- split-K: publish this slab's partial, last arriver finishes the tile
-  float* part = p.partial;
   if (n < p.N) {
 #pragma unroll
     for (int q = 0; q < MQ; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = 8 * q + 4 * h + i;
-        if (m < M) part[((int64_t)slab * p.part_rows + row0 + m) * p.N + n] = yacc[q][i];
+        if (m < M) y[(int64_t)m * p.N + n] = f2bf(yacc[q][i]);
       }
   }
-  __threadfence();
-  uint32_t old = 0;
-  if (lane == 0) old = atomicAdd(p.counters + tile, 1u);
-  old = __shfl(old, 0);
-  if (old != (uint32_t)(p.S - 1)) return;
-  __threadfence();
-  if (n < p.N) {
-#pragma unroll
-    for (int q = 0; q < MQ; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 8 * q + 4 * h + i;
-        if (m < M) {
-          float v = 0.f;
-          for (int sl = 0; sl < p.S; ++sl)
-            v += __hip_atomic_load(part + ((int64_t)sl * p.part_rows + row0 + m) * p.N + n, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-          y[(int64_t)m * p.N + n] = f2bf(v);
-        }
-      }
-  }
-  if (lane == 0) atomicExch(p.counters + tile, 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -436,7 +394,7 @@ __global__ __launch_bounds__(512) void qmv_kernel(QmvParams p) {
 
 static int pick_u(int G) { return (G % 4 == 0) ? 4 : 1; }
 
-QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
+QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   QmvConfig c{};
   const int G = (int)(K / gs);
   const int MQ = (int)((M + 7) / 8);
@@ -448,80 +406,59 @@ QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool s
   const int64_t lds_cap = 40 * 1024;
   int cps = chunks;  // chunks per slab
   while ((int64_t)cps * U * lds_per_group > lds_cap && cps > 1) cps = (cps + 1) / 2;
-  int nslab = (chunks + cps - 1) / cps;
   int NW = 4;
-  int S = nslab, S_inner = 1;
-  if (single_pass) {
-    S = 1;
-    S_inner = nslab;
-  } else {
-    // enough waves to keep HBM busy: aim for >= 2048 waves in flight
-    const int64_t target = 2048;
-    while (tiles * S * NW < target) {
-      if (NW < 8 && cps >= 2 * NW) { NW *= 2; continue; }
-      if (cps > 1) {
-        cps = (cps + 1) / 2;
-        S = (chunks + cps - 1) / cps;
-        continue;
-      }
-      break;
-    }
-  }
-  // tuning override: LISAQ_QMV_CFG="<chunks per slab>,<waves per workgroup>"
-  if (const char* env = getenv("LISAQ_QMV_CFG")) {
-    int ecps = 0, enw = 0;
-    if (sscanf(env, "%d,%d", &ecps, &enw) == 2 && ecps >= 1 && enw >= 1 && enw <= 8) {
-      cps = ecps < chunks ? ecps : chunks;
-      NW = enw;
-      S = single_pass ? 1 : (chunks + cps - 1) / cps;
-      if (single_pass) S_inner = (chunks + cps - 1) / cps;
-    }
-  }
   // each wave should get at least one chunk of a slab
   while (NW > 1 && NW > cps) NW >>= 1;
   c.U = U;
   c.MQ = MQ;
   c.NW = NW;
-  c.S = S;
-  c.S_inner = S_inner;
+  c.S = 1;
+  c.S_inner = (chunks + cps - 1) / cps;
   c.slab_groups = cps * U;
   c.tiles = (int)tiles;
   const QmvLds L = qmv_lds_layout(c.slab_groups, gs, (int)M, MQ, bits, NW);
   c.lds_bytes = L.total;
-  if (S > 1 && tiles > kQmvMaxTiles) {  // too many tiles for the counter region: one pass
-    S_inner = S;
-    S = 1;
-    c.S = 1;
-    c.S_inner = S_inner;
-  }
-  c.ws_bytes = (c.S > 1) ? kQmvCounterBytes + (size_t)c.S * M * N * 4 : 0;
+  c.ws_bytes = 0;
   c.kind = 0;
   c.tile_rows = 32;
   return c;
 }
 
-// Dispatcher.  The cross-workgroup split over K (S > 1) is kept for
-// completeness but not chosen: publishing partials across workgroups needs
+// Dispatcher.  (No kernel publishes partials across workgroups: that needs
 // agent-scope release/acquire, which on a multi-XCD MI355X writes back and
-// invalidates L2 and measured 3x slower than one pass per row tile.
+// invalidates L2 and measured 3x slower than one pass per row tile.)
 QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
-  const char* force = getenv("LISAQ_QMV_KERNEL");  // tuning: "32", "16", "t" (streaming), "d" (dot), "p" (persistent)
-  const char f = force ? force[0] : 0;
-  // One or two rows: the persistent kernel when there are enough rows to keep
-  // every wave busy (measured), else (one row) the workgroup dot kernel; more
-  // rows: the MFMA streaming kernel.
-  if (!single_pass && f != '3' && f != '1' && f != 't' && f != 'd' && M <= 2 && (N >= 16384 || f == 'p')) {
+  // path selection: "w" one-stream rows, "p" persistent, "d" dot, "t"
+  // streaming, "1" 16-row, "3" 32-row (a kernel that refuses the shape falls
+  // through to the next in this order)
+  const char f = path_char("LISAQ_QMV_KERNEL");
+  if (f) {
+    if (!single_pass && f == 'w' && qmvw_supported(M, N, K, gs, bits)) return qmvw_config(M, N, K, gs, bits);
+    if (!single_pass && (f == 'w' || f == 'p') && M <= 2) {
+      const QmvConfig c = qmvp_config(M, N, K, gs, bits);
+      if (c.kind == 4) return c;
+    }
+    if ((f == 'w' || f == 'p' || f == 'd') && qmvd_supported(M, N, K, gs, bits)) return qmvd_config(M, N, K, gs, bits);
+    if (f != '1' && f != '3' && qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits, !single_pass);
+    if (f != '3' && qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
+    return qmv32_config(M, N, K, gs, bits);
+  }
+  // One or two rows with enough rows of W to keep every wave busy: the
+  // persistent kernel; three to eight rows: the one-stream kernel; else one
+  // row: the workgroup dot kernel; otherwise the MFMA streaming kernel.
+  if (!single_pass && M <= 2 && N >= 16384) {
     const QmvConfig c = qmvp_config(M, N, K, gs, bits);
     if (c.kind == 4) return c;
   }
-  if (f != '3' && f != '1' && f != 't' && (M == 1 || f == 'd') && qmvd_supported(M, N, K, gs, bits))
-    return qmvd_config(M, N, K, gs, bits);
-  if (f != '3' && f != '1' && qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits, !single_pass);
-  if (f != '3' && qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
-  return qmv32_config(M, N, K, gs, bits, true);
+  if (!single_pass && M >= 3 && qmvw_supported(M, N, K, gs, bits)) return qmvw_config(M, N, K, gs, bits);
+  if (M == 1 && qmvd_supported(M, N, K, gs, bits)) return qmvd_config(M, N, K, gs, bits);
+  if (qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits, !single_pass);
+  if (qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
+  return qmv32_config(M, N, K, gs, bits);
 }
 
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
+  if (c.kind == 5) return qmvw_launch(stream, c, p, bits, gs, grid_x);
   if (c.kind == 4) return qmvp_launch(stream, c, p, bits, gs, grid_x);
   if (c.kind == 3) return qmvd_launch(stream, c, p, bits, gs, grid_x);
   if (c.kind == 2) return qmvt_launch(stream, c, p, bits, gs, grid_x);
@@ -529,7 +466,7 @@ int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, in
 }
 
 int qmv_lds_bytes_for(const QmvConfig& c, int gs, int M, int bits) {
-  if (c.kind == 4) return 0;
+  if (c.kind == 5 || c.kind == 4) return c.lds_bytes;
   if (c.kind == 3) return qmvd_lds_bytes(c, M);
   if (c.kind == 2) return qmvt_lds_bytes(c, gs, M, bits);
   return c.kind == 1 ? qmv16_lds_bytes(c.slab_groups, gs, M, c.MQ, bits, c.NW)

@@ -25,11 +25,6 @@
 #include <cstdio>
 #include <cstdlib>
 
-#ifdef LISAQ_EXPERIMENT
-#define DBG(bit) (p.debug & (bit))
-#else
-#define DBG(bit) 0
-#endif
 
 namespace lisaq {
 
@@ -204,7 +199,6 @@ __global__ __launch_bounds__(64 * NW) void qmv16_kernel(QmvParams p) {
         int i = ch * U + u;
         i = i < mine ? i : mine - 1;  // tail: reload a valid group (not used)
         // one base pointer per wave, compile-time offsets per group
-        if (DBG(8)) { wr[u] = WV{}; continue; }
         wr[u] = *reinterpret_cast<const WV*>(wbase + (int64_t)(NW * i) * (GS * BITS / 32));
       }
     };
@@ -221,7 +215,7 @@ __global__ __launch_bounds__(64 * NW) void qmv16_kernel(QmvParams p) {
       constexpr int SBE = 8;  // (row, group pair) items per thread and pass
       const bool pairs = ((p.G | g_begin | GL) & 1) == 0;
       const int per_row = pairs ? GL / 2 : GL;
-      const int sbe = DBG(2) ? 0 : 16 * per_row;
+      const int sbe = 16 * per_row;
       for (int base = 0; base < sbe; base += SBE * (int)blockDim.x) {
         uint32_t sv[SBE], bv[SBE];
 #pragma unroll
@@ -257,7 +251,7 @@ __global__ __launch_bounds__(64 * NW) void qmv16_kernel(QmvParams p) {
       // x: one item per (m, group, lane group); the lane groups of a group are
       // 4 adjacent lanes, so their partial sums combine by lane exchange
       constexpr int XE = 2;  // items per thread and pass
-      const int entries = DBG(1) ? 0 : M * GL * 4;
+      const int entries = M * GL * 4;
       float* xs = reinterpret_cast<float*>(xs4);
       for (int base = 0; base < entries; base += XE * (int)blockDim.x) {
         uint32_t raw[XE][HV / 2];
@@ -346,14 +340,6 @@ __global__ __launch_bounds__(64 * NW) void qmv16_kernel(QmvParams p) {
         const int ch = ch0 + d;
         if (ch >= nchunks) break;
         WV* wcur = wring[d];
-        if (DBG(4)) {
-          uint32_t acc_x = 0;
-#pragma unroll
-          for (int u = 0; u < U; ++u) acc_x ^= lane_word<WPL>(wcur[u], 0);
-          yacc[0][0] += (float)(acc_x & 1);
-          if (ch + D < nchunks) load_chunk(ch + D, wring[d]);
-          continue;
-        }
       f32x4_t acc[U][MQ];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -459,9 +445,9 @@ QmvConfig qmv16_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   if (SG < G) SG = ((SG + NW - 1) / NW) * NW;
   c.slab_groups = SG > G ? G : SG;
   c.S_inner = (G + c.slab_groups - 1) / c.slab_groups;
-  if (const char* env = getenv("LISAQ_QMV16_CFG")) {
-    int enw = 0, eu = 0;
-    if (sscanf(env, "%d,%d", &enw, &eu) >= 1 && (enw == 2 || enw == 4 || enw == 8)) c.NW = enw;
+  {
+    const int v = tune_int("LISAQ_QMV16_NW", c.NW);
+    if (v == 2 || v == 4 || v == 8) c.NW = v;
   }
   c.lds_bytes = qmv16_layout(c.slab_groups, gs, (int)M, MQ, bits, c.NW).total;
   c.ws_bytes = 0;
@@ -494,9 +480,6 @@ int qmv16_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, 
   p.S = 1;
   p.S_inner = c.S_inner;
   p.slab_groups = c.slab_groups;
-#ifdef LISAQ_EXPERIMENT
-  if (const char* d = getenv("LISAQ_DEBUG")) p.debug = atoi(d);
-#endif
   if (int rc = allow_dyn_lds((const void*)fn, c.lds_bytes, "qmv16")) return rc;
   hipLaunchKernelGGL(fn, dim3(grid_x), dim3(64 * c.NW), c.lds_bytes, stream, p);
   return check_launch("qmv16");

@@ -28,11 +28,6 @@
 
 #include <cstdlib>
 
-// experiment builds: compile-time switches that skip phases (never shipped)
-#ifndef QMVD_DBG
-#define QMVD_DBG 0
-#endif
-#define QDBG(bit) (QMVD_DBG & (bit))
 
 namespace lisaq {
 
@@ -148,7 +143,7 @@ __global__ __launch_bounds__(kQmvdMaxThreads) void qmvd_kernel(QmvParams p) {
     const u32x4* src = reinterpret_cast<const u32x4*>(x + (int64_t)mm * p.K + (int64_t)lc * CPC);
 #pragma unroll
     for (int i = 0; i < CPC / 8; ++i) {
-      const u32x4 v = QDBG(32) ? u32x4{(uint32_t)lc, 1u, 2u, 3u} : src[i];
+      const u32x4 v = src[i];
       raw[m][4 * i] = v[0];
       raw[m][4 * i + 1] = v[1];
       raw[m][4 * i + 2] = v[2];
@@ -168,7 +163,7 @@ __global__ __launch_bounds__(kQmvdMaxThreads) void qmvd_kernel(QmvParams p) {
 #pragma unroll
   for (int k = 0; k < kSbiMax; ++k) {
     sraw[k] = braw[k] = u32x2{0u, 0u};
-    if (!QDBG(1) && k < p.sbi) {
+    if (k < p.sbi) {
       const int e = 4 * (t + T * k);
       if (vec_ok && e + 4 <= Lv) {
         sraw[k] = *reinterpret_cast<const u32x2*>(sblk + e);
@@ -194,12 +189,8 @@ __global__ __launch_bounds__(kQmvdMaxThreads) void qmvd_kernel(QmvParams p) {
   for (int i = 0; i < LPT; ++i) {
     int r = n0 + i * RPR + rsub;
     r = r < p.N ? r : p.N - 1;
-    if (QDBG(8)) {  // skip the weight loads
-      for (int j = 0; j < WPC; ++j) wv[i][j] = (uint32_t)(r * 77 + j);
-    } else {
       wv[i] = __builtin_nontemporal_load(  // read once: nontemporal
           reinterpret_cast<const chunk_t*>(reinterpret_cast<const unsigned char*>(w) + r * rowbytes + lc * CB));
-    }
     // keep the issue order (x, s/b, then row by row) so each wait is exact
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -218,7 +209,7 @@ __global__ __launch_bounds__(kQmvdMaxThreads) void qmvd_kernel(QmvParams p) {
       }
     }
   }
-  if (!QDBG(1)) __syncthreads();
+  __syncthreads();
 
   // --- x paired in unpack order, with its sums (rows m >= M are zero)
   uint32_t xp[MR][NP];
@@ -268,10 +259,6 @@ __global__ __launch_bounds__(kQmvdMaxThreads) void qmvd_kernel(QmvParams p) {
 #pragma unroll
     for (int wd = 0; wd < WPC; ++wd) {
       uint32_t r[PPW];
-      if (QDBG(2)) {  // skip the arithmetic
-        d0[0] += (float)(wv[i][wd] & 1);
-        continue;
-      }
       unpack_pairs<BITS>(wv[i][wd], kc, r);
 #pragma unroll
       for (int j = 0; j < PPW; ++j)
@@ -295,12 +282,6 @@ __global__ __launch_bounds__(kQmvdMaxThreads) void qmvd_kernel(QmvParams p) {
   for (int m = 0; m < MR; ++m)
 #pragma unroll
     for (int i = 0; i < LPT; ++i) red[slot0 + m * mstride + i * istride] = part[m][i];
-  if (QDBG(16)) {  // skip the reduction: chunk 0 stores its partial
-    if (active && lc == 0)
-      for (int i = 0; i < LPT; ++i)
-        if (n0 + i * RPR + rsub < p.N) y[n0 + i * RPR + rsub] = f2bf(part[0][i]);
-    return;
-  }
   __syncthreads();
   // fixed order for every launch geometry (so any MR gives each row the same
   // bits): RSPLIT interleaved partial sums over the chunks, then their sum
@@ -353,11 +334,8 @@ QmvConfig qmvd_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
       best = nw;
     }
   }
-  c.NW = best;
-  if (const char* env = getenv("LISAQ_QMVD_NW")) {
-    const int v = atoi(env);
-    if (v >= 1 && v <= kQmvdMaxThreads / 64 && 64 * v >= C) c.NW = v;
-  }
+  c.NW = tune_int("LISAQ_QMVD_NW", best);
+  if (c.NW < 1 || c.NW > kQmvdMaxThreads / 64 || 64 * c.NW < C) return c;
   const int T = 64 * c.NW;
   c.S = T / C;  // rows side by side
   // rows per thread: 4, or 2 when 4 leaves fewer than 256 workgroups.
@@ -366,10 +344,8 @@ QmvConfig qmvd_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   // 8 8.6; 9728 x 2560 LPT 4 6.07 us, 2 6.89, 8 7.0.
   int lpt = 4;
   if ((N + (int64_t)c.S * lpt - 1) / ((int64_t)c.S * lpt) < 256) lpt = 2;
-  if (const char* env = getenv("LISAQ_QMVD_LPT")) {
-    const int v = atoi(env);
-    if (v == 2 || v == 4 || v == 8 || v == 16) lpt = v;
-  }
+  lpt = tune_int("LISAQ_QMVD_LPT", lpt);
+  if (lpt != 2 && lpt != 4 && lpt != 8 && lpt != 16) return c;
   // the tile's scales/biases must fit kSbiMax 4-element loads per thread
   auto sbi_of = [&](int l) { return (c.S * l * G + 4 * T - 1) / (4 * T); };
   while (lpt > 2 && sbi_of(lpt) > kSbiMax) lpt /= 2;

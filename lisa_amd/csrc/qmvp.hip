@@ -26,13 +26,6 @@
 #include "qmv.h"
 #include "qmv_dev.h"
 
-#include <cstdlib>
-
-// experiment builds: compile-time switches that skip phases (never shipped)
-#ifndef QMVP_DBG
-#define QMVP_DBG 0
-#endif
-#define PDBG(bit) (QMVP_DBG & (bit))
 
 namespace lisaq {
 
@@ -88,7 +81,7 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
       for (int i = 0; i < 4; ++i) {
         const u32x4 v = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rx, (ok && !PDBG(32)) ? (uint32_t)r * p.K * 2 + (uint32_t)c * 64 + 16 * i : kOob, 0, 0));
+                       rx, ok ? (uint32_t)r * p.K * 2 + (uint32_t)c * 64 + 16 * i : kOob, 0, 0));
         raw[r][j][4 * i] = v[0];
         raw[r][j][4 * i + 1] = v[1];
         raw[r][j][4 * i + 2] = v[2];
@@ -105,7 +98,7 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
     const bool ok = k < cnt;
     const int64_t row = ok ? gw + (int64_t)k * nwv : 0;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(reinterpret_cast<const unsigned char*>(p.w) + row * rowbytes,
-                                                (ok && !PDBG(8)) ? rowbytes : 0);  // (8: skip the weight loads)
+                                                ok ? rowbytes : 0);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s + row * G, ok ? 2 * G : 0);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + row * G, ok ? 2 * G : 0);
 #pragma unroll
@@ -115,7 +108,7 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
       else
         wv[slot][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b64(rw, woff[j], 0, kNt));
     }
-    const uint32_t o = (sb_lane && !PDBG(1)) ? sb_off : kOob;  // (1: skip the scale/bias loads)
+    const uint32_t o = sb_lane ? sb_off : kOob;
     static_assert(SBW == 16 || SBW == 4, "scale/bias load width");
     if constexpr (SBW == 16) {
       sv[slot] = __builtin_bit_cast(sbv_t, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kNt));
@@ -155,10 +148,6 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
       for (int r = 0; r < MR; ++r) d0[r] = d1[r] = 0.f;
 #pragma unroll
       for (int wd = 0; wd < WPC; ++wd) {
-        if (PDBG(2)) {  // skip the arithmetic
-          d0[0] += __uint_as_float(wv[slot][j][wd] & 0x3fffffu);
-          continue;
-        }
         uint32_t rq[PPW];
         punpack<BITS>(wv[slot][j][wd], kc, rq);
 #pragma unroll
@@ -212,22 +201,11 @@ QmvConfig qmvp_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
     return c;
   c.MR = (int)M;
   c.U = (int)((C + 63) / 64);  // J passes
-  c.S = 2;                     // ring depth D
-  if (const char* env = getenv("LISAQ_QMVP_D")) {
-    const int v = atoi(env);
-    if (v == 2 || v == 3) c.S = v;
-  }
-  int wgs_per_cu = 2;
-  if (const char* env = getenv("LISAQ_QMVP_WG")) {
-    const int v = atoi(env);
-    if (v >= 1 && v <= 16) wgs_per_cu = v;
-  }
+  c.S = tune_int("LISAQ_QMVP_D", 2);  // ring depth D
+  if (c.S != 2 && c.S != 3) return c;
   c.NW = 4;
-  int64_t grid = 256LL * wgs_per_cu;
-  if (const char* env = getenv("LISAQ_QMVP_GRID")) {  // tuning: workgroups
-    const int v = atoi(env);
-    if (v >= 64 && v <= 4096) grid = v;
-  }
+  const int64_t grid = tune_int("LISAQ_QMVP_GRID", 512);  // two workgroups per compute unit
+  if (grid < 64 || grid > 4096) return c;
   const int64_t need = (N + 3) / 4;
   c.tiles = (int)(grid < need ? grid : need);
   const int64_t waves = 4LL * c.tiles;

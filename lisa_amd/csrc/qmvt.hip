@@ -25,11 +25,6 @@
 #include <cstdio>
 #include <cstdlib>
 
-#ifdef LISAQ_EXPERIMENT
-#define XDBG(bit) (p.debug & (bit))
-#else
-#define XDBG(bit) 0
-#endif
 
 namespace lisaq {
 
@@ -230,7 +225,7 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
     // x staging, part 1: issue this thread's first pass of x loads before
     // the weight ring, so x does not queue behind the weight stream
     constexpr int XE = 2;
-    const int entries = XDBG(1) ? 0 : M * GL * 4;
+    const int entries = M * GL * 4;
     uint32_t xraw[XE][HV / 2];
     auto x_load = [&](int base) {
 #pragma unroll
@@ -265,7 +260,6 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
       const int64_t off = gfirst * GB;
 #pragma unroll
       for (int i = 0; i < IPS; ++i) {
-        if (XDBG(8)) { dst[i] = u32x4{(uint32_t)i, 0u, 0u, 0u}; continue; }
         dst[i] = *reinterpret_cast<const u32x4*>(lsrc[i] + off);
       }
     };
@@ -343,14 +337,6 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
       for (int d = 0; d < D; ++d) {
         const int j = j0 + d;
         if (j >= mine) break;
-        if (XDBG(16)) {
-          uint32_t xa = 0;
-#pragma unroll
-          for (int i = 0; i < IPS; ++i) xa ^= ring[d][i][0] ^ ring[d][i][3];
-          yacc[0][0] += (float)(xa & 1);
-          if (j + D < mine) load_slab(j + D, ring[d], sring[d], bring[d]);
-          continue;
-        }
         // re-layout this slab through the wave's LDS buffer (in-order per wave)
 #pragma unroll
         for (int i = 0; i < IPS; ++i) *reinterpret_cast<u32x4*>(wb + wslot[i]) = ring[d][i];
@@ -361,11 +347,6 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
           bf[gl] = sb_get<GPS>(bring[d], gl);
         }
         if (j + D < mine) load_slab(j + D, ring[d], sring[d], bring[d]);
-        if (XDBG(4)) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(wb + wslot[0]);
-          yacc[0][0] += (float)(v[1] & 1);
-          continue;
-        }
         const int gs0 = (wl + NW * j) * GPS;  // first group of the slab (in the x slab)
 #pragma unroll
         for (int gl = 0; gl < GPS; ++gl) {
@@ -476,8 +457,7 @@ __global__ __launch_bounds__(256) void qmvt_split_reduce_kernel(const float* __r
 static int pick_sb(int64_t K, int gs, int bits) {
   const int64_t rowbytes = K * bits / 8;
   const int gb = gs * bits / 8;
-  int sb = 128;
-  if (const char* env = getenv("LISAQ_QMVT_SB")) sb = atoi(env) == 256 ? 256 : 128;
+  const int sb = tune_int("LISAQ_QMVT_SB", 128) == 256 ? 256 : 128;
   if (sb == 256 && rowbytes % 256 == 0 && 256 % gb == 0) return 256;
   if (rowbytes % 128 == 0 && 128 % gb == 0) return 128;
   return 0;
@@ -501,12 +481,7 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   c.tiles = (int)((N + 15) / 16);
   c.NW = 4;
   if (c.tiles * 4 < 2048 && nws >= 16) c.NW = 8;
-  if (const char* env = getenv("LISAQ_QMVT_NW")) {  // tuning: 4 or 8
-    // (2 waves per tile gave run-to-run differing bits in a sweep, cause not
-    // found: not offered)
-    const int v = atoi(env);
-    if (v == 4 || v == 8) c.NW = v;
-  }
+  c.NW = tune_int("LISAQ_QMVT_NW", c.NW) == 8 ? 8 : 4;
   // x slab: at most ~40 KB of staged x, a whole number of W slabs
   const int64_t per_group = (int64_t)gs * M * 2;
   int SG = G;
@@ -517,8 +492,8 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   // (measured at N = 17408: 4 rows 23.3 -> 20.6 us, 8 rows 26.3 -> 25.4 us;
   // slower at N = 9728)
   c.tpb = (M >= 2 && M <= 8 && c.NW == 4 && c.tiles >= 1024) ? 2 : 1;
-  if (const char* env = getenv("LISAQ_QMVT_TPB")) {  // tuning: 1 or 2
-    const int v = atoi(env);
+  {
+    const int v = tune_int("LISAQ_QMVT_TPB", c.tpb);
     if (v == 1 || (v == 2 && c.NW <= 4)) c.tpb = v;
   }
   // Fewer blocks than compute units (e.g. N = 2560: 160 row tiles): split K
@@ -530,10 +505,8 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   if (allow_split && M >= 4) {
     const int blocks = (c.tiles + c.tpb - 1) / c.tpb;
     int S = blocks < 256 ? (M >= 8 ? 4 : 3) : 1;
-    if (const char* env = getenv("LISAQ_QMVT_SPLIT")) {  // tuning: parts (1 disables)
-      const int v = atoi(env);
-      if (v >= 1 && v <= 8) S = v;
-    }
+    S = tune_int("LISAQ_QMVT_SPLIT", S);
+    if (S < 1) S = 1;
     if (S > 4) S = 4;
     if (S > 1) {
       int sg = (G + S - 1) / S;
@@ -548,7 +521,7 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   c.slab_groups = SG;
   c.S_inner = (G + SG - 1) / SG;
   c.lds_bytes = qmvt_layout(SG, gs, (int)M, c.MQ, bits, c.NW * c.tpb, SB).total;
-  c.ws_bytes = c.S > 1 ? kQmvCounterBytes + (size_t)c.S * M * N * 4 : 0;
+  c.ws_bytes = c.S > 1 ? (size_t)c.S * M * N * 4 : 0;
   c.kind = 2;
   c.tile_rows = 16;
   return c;
@@ -594,9 +567,6 @@ int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
   p.S = p.tiles ? 1 : c.S;
   p.S_inner = c.S_inner;
   p.slab_groups = c.slab_groups;
-#ifdef LISAQ_EXPERIMENT
-  if (const char* d = getenv("LISAQ_DEBUG")) p.debug = atoi(d);
-#endif
   // tile-table launches: one tile per block (the table gives each block its tile)
   const int tpb = p.tiles ? 1 : (c.tpb > 0 ? c.tpb : 1);
   int lds = c.lds_bytes;

@@ -48,9 +48,6 @@ def workspace(device: torch.device, nbytes: int, kind: str = "linear") -> torch.
         return buf
 
 
-QMV_COUNTER_BYTES = 32768 * 4  # fixed counter region at the start of the linear workspace
-
-
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -106,9 +103,6 @@ def _mm(entry: str, x, w, scales, biases, transpose, group_size, bits):
     lib = _lib.load()
     if entry == "lisaq_qmm":
         nbytes = lib.lisaq_qmm_workspace(M, N, K, group_size, bits)
-    elif entry == "lisaq_quantized_matmul_serial_rows":
-        nbytes = lib.lisaq_quantized_matmul_workspace(1, N, K, group_size, bits)
-        nbytes = nbytes and nbytes + (M - 1) * (nbytes - QMV_COUNTER_BYTES)
     else:
         nbytes = lib.lisaq_quantized_matmul_workspace(M, N, K, group_size, bits)
     ws = workspace(x.device, nbytes)

@@ -27,8 +27,13 @@ QMV_CASES = [
     (3, 64, 512, 4, 64),         # array_ops.rs:650-710 shape
     (1, 100, 512, 4, 64),        # N tail (not a multiple of 32)
     (5, 77, 320, 4, 64),         # K/gs = 5 groups (U = 1 path), N tail
-    (2, 9728, 2560, 4, 64),      # configs[1] up
-    (8, 2560, 9728, 4, 64),      # configs[1] down (split over K)
+    (1, 9728, 2560, 4, 64),      # configs[1] up
+    (2, 9728, 2560, 4, 64),
+    (4, 9728, 2560, 4, 64),
+    (8, 9728, 2560, 4, 64),
+    (1, 2560, 9728, 4, 64),      # configs[1] down
+    (2, 2560, 9728, 4, 64),
+    (8, 2560, 9728, 4, 64),      # (split over K)
     (4, 2560, 9728, 4, 64),
     (1, 512, 1024, 2, 64),
     (8, 640, 2048, 2, 64),
@@ -56,7 +61,7 @@ def test_qmv_parity(dev, oracle, M, N, K, bits, gs):
         assert np.array_equal(got, got2)
 
 
-@pytest.mark.parametrize("kernel", ["p", "d", "t", "16", "32"])
+@pytest.mark.parametrize("kernel", ["w", "p", "d", "t", "16", "32"])
 @pytest.mark.parametrize("M,N,K,bits,gs", [
     (1, 100, 1024, 4, 64),      # fewer rows than waves (persistent kernel), J = 1
     (1, 4099, 2560, 4, 64),     # J = 2, N tail
@@ -114,7 +119,8 @@ def test_qmm_split_k(dev, oracle, monkeypatch, split):
     assert np.array_equal(_run(ops.qmm, dev, x, w, s, b, 64, 4), got)
 
 
-@pytest.mark.parametrize("M,N,K,bits", [(128, 17408, 5120, 4), (512, 5120, 17408, 4), (2048, 17408, 5120, 4),
+@pytest.mark.parametrize("M,N,K,bits", [(128, 17408, 5120, 4), (128, 5120, 17408, 4), (512, 17408, 5120, 4),
+                                        (512, 5120, 17408, 4), (2048, 17408, 5120, 4), (2048, 5120, 17408, 4),
                                         (512, 17408, 5120, 2)])
 def test_qmm_prefill_shapes_sampled_rows(dev, oracle, M, N, K, bits):
     """configs[2]/[3] prefill shapes; the oracle checks 8 sampled rows (every column)."""
@@ -134,10 +140,12 @@ def test_qmm_prefill_shapes_sampled_rows(dev, oracle, M, N, K, bits):
 
 
 @pytest.mark.parametrize("M", [4, 8])
-def test_qmv_split_k_and_its_fallback(dev, oracle, M):
+def test_qmv_split_k_and_its_fallback(dev, oracle, monkeypatch, M):
     """Few row tiles (N = 2560): the streaming matvec splits K over workgroups when the workspace holds
     the parts; given none, the same call runs unsplit. Both against the oracle, and close to each other."""
     import torch
+
+    monkeypatch.setenv("LISAQ_QMV_KERNEL", "t")
 
     from lisa_amd import _lib
 
@@ -181,6 +189,37 @@ def test_north_star_qmv_shape(dev, oracle, bits):
         got = _run(ops.quantized_matmul, dev, x, w, s, b, 64, bits)
         assert_close_bf16(got, ref, what=f"north-star qmv M={M} bits={bits}")
         assert np.array_equal(_run(ops.quantized_matmul, dev, x, w, s, b, 64, bits), got)
+
+
+@pytest.mark.parametrize("N,K,gs", [(17408, 5120, 64), (9728, 2560, 64), (2560, 9728, 64), (1000, 1024, 64),
+                                    (777, 2048, 128), (5, 512, 64)])
+def test_one_stream_rows_bitwise(dev, oracle, monkeypatch, N, K, gs):
+    """The one-stream matvec (1..8 rows of x on one pass over W): every row of an M-row call is bitwise
+    equal to the same kernel's one-row call (the matrix-core column of a row never mixes other rows), for
+    every M; every row within tolerance of the oracle.  (Where the staged rows of x do not fit its LDS --
+    eight rows at K = 9728 -- the call takes another kernel: those rows are only checked against the
+    oracle.)"""
+    monkeypatch.setenv("LISAQ_QMV_KERNEL", "w")
+    rng = np.random.default_rng(N + K + gs)
+    w, s, b = np_linear(rng, N, K, 4, gs)
+    x = np_x(rng, 8, K)
+    ref = oracle.qmv(x, w, s, b, gs, 4)
+    ones = np.concatenate([_run(ops.qmv, dev, x[r:r + 1], w, s, b, gs, 4) for r in range(8)])
+    assert_close_bf16(ones, ref, what=f"one-stream M=1 N={N} K={K}")
+    for M in range(2, 9):
+        got = _run(ops.qmv, dev, x[:M], w, s, b, gs, 4)
+        assert_close_bf16(got, ref[:M], what=f"one-stream M={M} N={N} K={K}")
+        if _one_stream_fits(M, N, K):
+            assert np.array_equal(got, ones[:M]), (N, K, M)
+
+
+def _one_stream_fits(M, N, K):
+    """LDS bytes of the one-stream matvec at its default grid (256 workgroups) within 160 KB: staged
+    rows of x (+ one zero row), block sums, per-unit partials (qmvw.hip, qmvw_lds)."""
+    MP = 1 if M == 1 else 2 if M == 2 else 4 if M <= 4 else 8
+    RP = min(MP, 4)
+    T = (-(-N // 256) + 15) // 16
+    return (MP + 1) * (2 * K + 16) + (K // 64) * MP * 4 + T * (K // 512) * 64 * RP * 4 <= 160 * 1024
 
 
 @pytest.mark.parametrize("bits", [2, 4])

@@ -165,6 +165,57 @@ def test_moe_forward_parity(dev, oracle, T):
     torch.cuda.synchronize()
 
 
+def _run_ref(oracle, xr, W, S, B, e, limit):
+    """One run of expert e as the reference's per-run loop computes it (array_ops.rs:591-630)."""
+    fn = oracle.qmv if xr.shape[0] < limit else oracle.qmm
+    return fn(xr, W[e], S[e], B[e], 64, 4)
+
+
+def test_moe_forward_baseline_shape(dev, oracle):
+    """BASELINE configs[4] at T=4096 (E=128, k=8, H=2048, I=768; 32768 routed rows, ~256-row expert runs
+    through the matmul tiles): routing bit-exact; the gate, up and down gather_qmm of four sampled experts'
+    whole runs (all columns) against the per-run oracle; moe_forward bitwise equal to its steps composed
+    from the public entry points; 64 sampled tokens of the combine bit-exact against the oracle's combine."""
+    import torch
+
+    rng = np.random.default_rng(4096)
+    T, E, k, H, I = 4096, 128, 8, 2048, 768
+    G, U, D = _expert_stack(rng, E, I, H), _expert_stack(rng, E, I, H), _expert_stack(rng, E, H, I)
+    x = np_x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
+    xd, lgd = to_dev_bf16(x, dev), to_dev(lg, dev)
+    out, idx, wts = ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, return_routing=True)
+    ridx, rw = oracle.topk_route(lg, k)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+    srt, order, rows, inv, offs = oracle.moe_sort(ridx.reshape(-1), E, k)
+    # device pieces (public entry points) on the same sorted rows
+    sid = to_dev(srt, dev)
+    xs_d = ops.gather_rows(xd, to_dev(rows, dev))
+    gd = ops.gather_qmm(xs_d, *dv[0], rhs_indices=sid)
+    ud = ops.gather_qmm(xs_d, *dv[1], rhs_indices=sid)
+    act = ops.swiglu(gd, ud)
+    dd = ops.gather_qmm(act, *dv[2], rhs_indices=sid)
+    comb = ops.moe_combine(dd, wts.reshape(-1), to_dev(inv, dev), T, k)
+    assert torch.equal(out.view(torch.int16), comb.view(torch.int16))
+    xs, g_h, u_h, a_h, d_h = (from_dev_bf16(t) for t in (xs_d, gd, ud, act, dd))
+    assert np.array_equal(xs, x[rows])
+    lim_gu, lim_d = ops.qmv_batch_limit(H, I), ops.qmv_batch_limit(I, H)
+    sizes = np.diff(offs)
+    picks = [int(np.argmax(sizes)), int(np.argmin(np.where(sizes > 0, sizes, 1 << 30))), 0, E - 1]
+    for e in picks:
+        a, b = offs[e], offs[e + 1]
+        if a == b:
+            continue
+        assert_close_bf16(g_h[a:b], _run_ref(oracle, xs[a:b], *G, e, lim_gu), what=f"gate expert {e} ({b - a} rows)")
+        assert_close_bf16(u_h[a:b], _run_ref(oracle, xs[a:b], *U, e, lim_gu), what=f"up expert {e}")
+        assert_close_bf16(d_h[a:b], _run_ref(oracle, a_h[a:b], *D, e, lim_d), what=f"down expert {e}")
+    tok = np.sort(rng.choice(T, 64, replace=False))
+    ref = oracle.moe_combine(d_h, wts.cpu().numpy(), inv, T, k)
+    assert np.array_equal(from_dev_bf16(out)[tok], ref[tok])
+
+
 @pytest.mark.parametrize("T,E,k,H,I,bits,gs", [(1, 128, 8, 2048, 768, 4, 64), (3, 16, 4, 512, 256, 4, 32),
                                              (8, 32, 2, 1024, 384, 4, 128), (2, 64, 8, 256, 768, 2, 64),
                                              (5, 32, 16, 128, 1024, 2, 128), (1, 4, 1, 4096, 64, 4, 64)])
