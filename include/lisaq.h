@@ -76,6 +76,20 @@ LISAQ_API int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t
                            size_t workspace_bytes);
 LISAQ_API size_t lisaq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 
+/* lisaq_quantized_matmul without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split-K partials live in a 64 MiB device array built into the library
+ * (each GPU the library runs on holds its own copy until the process ends);
+ * the call allocates nothing.  Every split this library chooses fits it; a
+ * shape that would need more fails with LISAQ_EWORKSPACE.  Nothing in the
+ * scratch needs to start at zero (every part is written before it is read).
+ * Calls that overlap on one GPU (two streams, or two host threads) share the
+ * scratch and race: order them on one stream. */
+LISAQ_API int lisaq_quantized_matmul_noalloc(void* stream, const void* x, const uint32_t* w, const void* scales,
+                                   const void* biases, void* y, int64_t M, int64_t N, int64_t K,
+                                   int transpose, int group_size, int bits);
+
 /* Replaces ops::quantized_matmul_serial_rows (AO:500-555): each of the M<=8
  * rows gets the same arithmetic as an independent M=1 call (bitwise), and
  * M outside 2..8 falls back to lisaq_quantized_matmul. */

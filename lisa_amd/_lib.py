@@ -45,6 +45,7 @@ SIGNATURES = {
     "lisaq_last_error": (ctypes.c_char_p, []),
     "lisaq_quantized_matmul": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci, vp, sz]),
     "lisaq_quantized_matmul_workspace": (sz, [i64, i64, i64, ci, ci]),
+    "lisaq_quantized_matmul_noalloc": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci]),
     "lisaq_qmm_workspace": (sz, [i64, i64, i64, ci, ci]),
     "lisaq_quantized_matmul_serial_rows": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci, vp, sz]),
     "lisaq_qmv": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, vp, sz]),

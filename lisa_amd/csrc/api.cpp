@@ -232,6 +232,36 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
   return LISAQ_OK;
 }
 
+// Device scratch of lisaq_quantized_matmul_noalloc: the f32 split-K partials
+// of the matmul (and of the streaming matvec's split), which other entry
+// points take from a caller workspace.  Every split layout needs at most
+// 64 MiB (the matmul's hybrid split: at most 256 parts of 256 x 256 f32; its
+// small-grid split: parts x M x N x 4 <= 256 x 128 x 256 x 4).  The array's
+// name is only a host-side stand-in: host code uses the address that
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Address of `scratch` on the current device, looked up once per device.
+static int scratch_address(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(LISAQ_EHIP, "quantized_matmul_noalloc: no usable current device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(LISAQ_EHIP, "quantized_matmul_noalloc: scratch address: %s", hipGetErrorString(e));
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return LISAQ_OK;
+}
+
 }  // namespace lisaq
 
 using namespace lisaq;
@@ -327,6 +357,21 @@ int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t* w, const
     return run_qmv((hipStream_t)stream, c, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
   }
   return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
+}
+
+int lisaq_quantized_matmul_noalloc(void* stream, const void* x, const uint32_t* w, const void* s, const void* b,
+                                   void* y, int64_t M, int64_t N, int64_t K, int transpose, int gs, int bits) {
+  g_err[0] = 0;
+  int rc = validate_mm("quantized_matmul_noalloc", x, w, s, b, y, M, N, K, transpose, gs, bits);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return LISAQ_OK;
+  const size_t need = lisaq_quantized_matmul_workspace(M, N, K, gs, bits);
+  LISAQ_REQUIRE(need <= kScratchBytes, LISAQ_EWORKSPACE,
+                "quantized_matmul_noalloc: needs %zu bytes of scratch, more than the %zu-byte device scratch", need,
+                kScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  return lisaq_quantized_matmul(stream, x, w, s, b, y, M, N, K, transpose, gs, bits, ws, kScratchBytes);
 }
 
 int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32_t* w, const void* s,
