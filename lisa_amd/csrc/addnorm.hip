@@ -5,14 +5,16 @@
 //
 // Per row of x (one workgroup each):
 //   s      = bf16(f32(x) + f32(r))                      -> sum_out
-//   inv    = 1 / sqrt(sum(f32(s)^2) / K + eps)          (f32)
+//   inv    = rsqrt(f32(sum(f32(s)^2) / K) + eps)        (f32, rounded once)
 //   normed = bf16(f32(nw) * f32(bf16(f32(s) * inv)))    -> norm_out
 // the rounding chain of norm_qmv.metal:383-400; the matvec then reads
 // norm_out.  The sum of squares is a fixed-order f32 reduction (each thread
 // strided over K, then the wave butterfly, then the four waves in order); the
 // reference reproduces Apple's simd_sum tree instead, so inv can differ in
 // its last bit, and a normed value by one bf16 step where s*inv sits on a
-// rounding boundary.  The row is 2*K bytes read twice plus 4*K written: a
+// rounding boundary.  The outputs must not overlap the inputs (checked by
+// the entry point).  The persistent matvec shapes fold this prologue into
+// the matvec kernel (qmvp.hip); this kernel serves the others.  The row is 2*K bytes read twice plus 4*K written: a
 // few microseconds at decode sizes, launch-bound, not HBM-bound.
 #include "kernels.h"
 #include "lisaq_common.h"
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(256) void add_rms_kernel(const u32x4* __restrict__ 
       const float lo = add_bf16(a[w], b[w], 0), hi = add_bf16(a[w], b[w], 1);
       ss = fmaf(lo, lo, ss);
       ss = fmaf(hi, hi, ss);
-      o[w] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+      o[w] = pack_bf2(lo, hi);
     }
     sum_out[base + i] = o;
   }
@@ -53,7 +55,8 @@ __global__ __launch_bounds__(256) void add_rms_kernel(const u32x4* __restrict__ 
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-  const float inv = 1.0f / sqrtf(total / (float)K + eps);
+  // rsqrt(total / K + eps) with one rounding (metal::precise::rsqrt)
+  const float inv = (float)(1.0 / sqrt((double)(total / (float)K + eps)));
 #pragma unroll 4
   for (int i = threadIdx.x; i < KV; i += 256) {
     const u32x4 a = x[base + i], b = r[base + i], g = nw[i];
@@ -62,7 +65,7 @@ __global__ __launch_bounds__(256) void add_rms_kernel(const u32x4* __restrict__ 
     for (int w = 0; w < 4; ++w) {
       const float tlo = bf2f(f2bf(add_bf16(a[w], b[w], 0) * inv));
       const float thi = bf2f(f2bf(add_bf16(a[w], b[w], 1) * inv));
-      o[w] = (uint32_t)f2bf(bf2f_lo(g[w]) * tlo) | ((uint32_t)f2bf(bf2f_hi(g[w]) * thi) << 16);
+      o[w] = pack_bf2(bf2f_lo(g[w]) * tlo, bf2f_hi(g[w]) * thi);
     }
     norm_out[base + i] = o;
   }

@@ -468,11 +468,39 @@ int lisaq_qmv_addnorm(void* stream, const void* x, const void* r, const void* no
   LISAQ_REQUIRE(aligned(x, 16) && aligned(r, 16) && aligned(norm_w, 16) && aligned(sum_out, 16) &&
                     aligned(norm_out, 16),
                 LISAQ_EINVAL_LAYOUT, "qmv_addnorm: x, r, norm weight, sum and norm rows must be 16-byte aligned");
+  // the outputs are written while other workgroups still read the inputs: no overlap allowed
+  auto overlaps = [&](const void* a, const void* b2) {
+    const uintptr_t p0 = (uintptr_t)a, q0 = (uintptr_t)b2, n = (uintptr_t)(M * K * 2);
+    return p0 < q0 + n && q0 < p0 + n;
+  };
+  LISAQ_REQUIRE(!overlaps(sum_out, x) && !overlaps(sum_out, r) && !overlaps(norm_out, x) && !overlaps(norm_out, r) &&
+                    !overlaps(sum_out, norm_out) && !overlaps(sum_out, norm_w) && !overlaps(norm_out, norm_w),
+                LISAQ_EINVAL_LAYOUT, "qmv_addnorm: sum_out and norm_out must not overlap each other or x, r, norm_w");
   hipStream_t st = (hipStream_t)stream;
+  const QmvConfig c = qmv_config(M, N, K, gs, bits);
+  if (c.kind == 4) {
+    // the persistent matvec takes the add + RMSNorm as its prologue: one launch
+    QmvParams p{};
+    p.x = (const uint16_t*)x;
+    p.w = w;
+    p.s = (const uint16_t*)s;
+    p.b = (const uint16_t*)b;
+    p.y = (uint16_t*)y;
+    p.M = 1;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.G = (int)(K / gs);
+    p.r = (const uint16_t*)r;
+    p.nw = (const uint16_t*)norm_w;
+    p.sum_out = (uint16_t*)sum_out;
+    p.norm_out = (uint16_t*)norm_out;
+    p.eps = eps;
+    return qmvp_addnorm_launch(st, c, p, bits, gs);
+  }
   if (int rc = launch_add_rms(st, (const uint16_t*)x, (const uint16_t*)r, (const uint16_t*)norm_w,
                               (uint16_t*)sum_out, (uint16_t*)norm_out, M, K, eps))
     return rc;
-  return run_qmv(st, qmv_config(M, N, K, gs, bits), norm_out, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
+  return run_qmv(st, c, norm_out, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
 }
 
 int lisaq_quantize(void* stream, const void* w, int dtype, uint32_t* wq, void* s, void* b, int64_t rows,

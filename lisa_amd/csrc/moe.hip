@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256) void swiglu8_kernel(const u32x4* __restrict__ 
   for (int j = 0; j < 4; ++j) {
     const float lo = __fmul_rn(silu_bf16(bf2f_lo(gv[j])), bf2f_lo(uv[j]));
     const float hi = __fmul_rn(silu_bf16(bf2f_hi(gv[j])), bf2f_hi(uv[j]));
-    o[j] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    o[j] = pack_bf2(lo, hi);
   }
   out[i] = o;
 }
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restric
   }
   u32x4 o;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) o[c] = (uint32_t)f2bf(total[2 * c]) | ((uint32_t)f2bf(total[2 * c + 1]) << 16);
+  for (int c = 0; c < 4; ++c) o[c] = pack_bf2(total[2 * c], total[2 * c + 1]);
   reinterpret_cast<u32x4*>(out + t * H)[d8] = o;
 }
 

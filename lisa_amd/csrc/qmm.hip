@@ -32,8 +32,8 @@ __global__ __launch_bounds__(256) void qmm_hybrid_reduce_kernel(const float* __r
   }
   uint16_t* dst = y + (int64_t)m * N + n;
   if (n + 3 < N && (N & 3) == 0) {
-    *reinterpret_cast<u32x2*>(dst) = u32x2{(uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
-                                           (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16)};
+    *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf2(v[0], v[1]),
+                                           pack_bf2(v[2], v[3])};
   } else {
     for (int c = 0; c < 4; ++c)
       if (n + c < N) dst[c] = f2bf(v[c]);
@@ -152,6 +152,11 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
     return qmm_launch(stream, c1, p, bits, gs, c1.grid, grid_y, nullptr, 0);
   }
   LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
+  // the two split layouts: per-part [S][M][N] partials with 128-row tiles,
+  // hybrid compact parts with 256-row tiles
+  if (split && !((c.full_tiles == 0 && c.MT == 4) || (c.full_tiles > 0 && c.MT == 8)))
+    return set_error(LISAQ_EUNSUPPORTED, "qmm: split over K with %d-row tiles (%s layout) is not built", 32 * c.MT,
+                     c.full_tiles > 0 ? "hybrid" : "per-part");
   int lds = 0;
   qmm_fn fn = split ? qmm_pick<true>(c, bits, gs, &lds) : qmm_pick<false>(c, bits, gs, &lds);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm: bits=%d group_size=%d not supported", bits, gs);

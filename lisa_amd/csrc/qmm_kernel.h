@@ -543,8 +543,13 @@ qmm_fn qmm_get_impl(int gs, int MT, int* lds) {
     if (gs == 128) return qmm_kernel<BITS, 128, M_, 1, 8, SPLIT>;
     return nullptr;
   };
+  // split launches exist in two layouts only: per-part partials [S][M][N]
+  // with 128-row tiles (small grids) and the hybrid compact layout with
+  // 256-row tiles; no other tile height is built with split output
   if (MT == 8) return one(std::integral_constant<int, 8>{});
-  if (MT == 6) return one(std::integral_constant<int, 6>{});
+  if constexpr (!SPLIT) {
+    if (MT == 6) return one(std::integral_constant<int, 6>{});
+  }
   if (MT == 4) return one(std::integral_constant<int, 4>{});
   return nullptr;
 }

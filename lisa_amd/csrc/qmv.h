@@ -21,6 +21,14 @@ struct QmvParams {
   int chunks, rpr, tile_rows;  // dot kernel: 32-code chunks per row, rows side by side, rows per tile
   int sbi;               // dot kernel: 4-element scale/bias staging loads per thread
   // filled by qmv_launch from the config
+  // residual add + RMSNorm folded into the persistent one-row kernel: x is
+  // the residual input, r the residual, nw the norm weight [K]; the sum row
+  // and the normed row (the matvec's input) are written to sum_out/norm_out
+  const uint16_t* r;
+  const uint16_t* nw;
+  uint16_t* sum_out;
+  uint16_t* norm_out;
+  float eps;
 };
 
 
@@ -70,6 +78,9 @@ QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
 bool qmvw_supported(int64_t M, int64_t N, int64_t K, int gs, int bits);
 int qmvw_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmvp_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
+// the persistent kernel with the residual add + RMSNorm prologue (p.r, p.nw,
+// p.sum_out, p.norm_out, p.eps set; one row; c from qmvp_config(1, ...))
+int qmvp_addnorm_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs);
 
 // Enqueue; grid_x = number of row tiles (or tile-table entries).
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);

@@ -31,11 +31,28 @@ namespace lisaq {
 
 using namespace qmvdev;
 
+// workgroup barrier for LDS traffic only: s_waitcnt lgkmcnt(0) (vector
+// memory counters left alone), then s_barrier
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+}
+
 // MR rows of x (1 or 2) share the weight stream: each W word is unpacked once
 // and dotted with every row's x; each row's arithmetic is exactly the one-row
 // kernel's (same lanes, same order), so its result is bitwise the same.
-template <int BITS, int GS, int J, int D, int SBW, int MR>
+//
+// AN (add+norm, one row): x and the residual r are added (s = bf16(x + r)),
+// every wave sums s^2 over the whole row itself (a wave covers all of K), so
+// inv = rsqrt(mean(s^2) + eps) needs no communication between workgroups;
+// the lane's x values become normed = bf16(nw * bf16(s * inv)), and wave 0
+// writes the sum and normed rows.  The matvec then runs on the normed row
+// with the one-row arithmetic, so y equals a plain call on norm_out bitwise
+// (jit::affine_qmv_fast_addnorm, crates/lisa-mlx/src/jit/matmul.rs:315-443,
+// norm_qmv.metal:293-423).
+template <int BITS, int GS, int J, int D, int SBW, int MR, bool AN = false>
 __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
+  static_assert(!AN || (MR == 1 && BITS == 4), "add+norm: one row, 4 bits");
   // SBW: bytes per lane of the two loads that bring a row's scales and
   // biases (lanes [0, SBL)); they pass through LDS to the lanes that use them
   typedef uint32_t sbv_t __attribute__((ext_vector_type(SBW >= 4 ? SBW / 4 : 1)));
@@ -75,18 +92,20 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
     const bool ok = c < C;
     woff[j] = ok ? (uint32_t)c * CB : kOob;
     gofs[j] = ok ? (c * 32 / GS) * 2 : 0;
+    if constexpr (!AN) {  // (add+norm: the normed x comes from LDS below)
 #pragma unroll
-    for (int r = 0; r < MR; ++r)
+      for (int r = 0; r < MR; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u32x4 v = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rx, ok ? (uint32_t)r * p.K * 2 + (uint32_t)c * 64 + 16 * i : kOob, 0, 0));
-        raw[r][j][4 * i] = v[0];
-        raw[r][j][4 * i + 1] = v[1];
-        raw[r][j][4 * i + 2] = v[2];
-        raw[r][j][4 * i + 3] = v[3];
-      }
+        for (int i = 0; i < 4; ++i) {
+          const u32x4 v = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         rx, ok ? (uint32_t)r * p.K * 2 + (uint32_t)c * 64 + 16 * i : kOob, 0, 0));
+          raw[r][j][4 * i] = v[0];
+          raw[r][j][4 * i + 1] = v[1];
+          raw[r][j][4 * i + 2] = v[2];
+          raw[r][j][4 * i + 3] = v[3];
+        }
+    }
   }
 
   // --- ring of D rows in flight
@@ -121,6 +140,80 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
 
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) issue(d, d);
+
+  // (add+norm) the sum and normed rows this thread stores after the main
+  // loop: a store before it would sit among the ring's loads in the memory
+  // counter and make the loop's waits conservative
+  u32x4 an_sum[3], an_norm[3];
+  if constexpr (AN) {
+    // Residual add + RMSNorm, once per workgroup: thread t takes the 16-byte
+    // blocks t, t + 256, t + 512 of the row (x, r and the norm weight all
+    // issued at once), the sum of squares in a fixed order (thread's blocks,
+    // words, low half then high half; wave sum; the four waves in order), the
+    // normed row to LDS, and each lane reads its chunks back from there.
+    static_assert(J <= 3, "add+norm: K <= 6144 (three blocks per thread)");
+    const int KB = p.K / 8;
+    const int tid = threadIdx.x;
+    unsigned char* an = reinterpret_cast<unsigned char*>(lds_res + (blockDim.x >> 6) * p.tile_rows * MR) +
+                        (blockDim.x >> 6) * 2 * G2;  // [K] bf16 normed row, then 4 wave sums
+    float* wsum = reinterpret_cast<float*>(an + 2 * p.K);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.r, (uint32_t)p.K * 2);
+    const __amdgpu_buffer_rsrc_t rn = make_rsrc(p.nw, (uint32_t)p.K * 2);
+    u32x4 xv[3], rv[3], gv[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int i = tid + 256 * q;
+      const uint32_t o = i < KB ? (uint32_t)i * 16 : kOob;
+      xv[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+      rv[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, o, 0, 0));
+      gv[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rn, o, 0, 0));
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t sw = pack_bf2(bf2f_lo(xv[q][e]) + bf2f_lo(rv[q][e]), bf2f_hi(xv[q][e]) + bf2f_hi(rv[q][e]));
+        const float lo = bf2f_lo(sw), hi = bf2f_hi(sw);
+        ss = fmaf(lo, lo, ss);
+        ss = fmaf(hi, hi, ss);
+        xv[q][e] = sw;  // the sum row
+      }
+    const float wtot = wave_sum(ss);
+    if (lane == 0) wsum[wave] = wtot;
+    // LDS-only barriers: __syncthreads() would also wait for the weight
+    // rows already in flight (and for the stores below)
+    lds_barrier();
+    const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    // rsqrt(total / K + eps) with one rounding (metal::precise::rsqrt)
+    const float inv = (float)(1.0 / sqrt((double)(total / (float)p.K + p.eps)));
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int i = tid + 256 * q;
+      u32x4 nv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t t = pack_bf2(bf2f_lo(xv[q][e]) * inv, bf2f_hi(xv[q][e]) * inv);
+        nv[e] = pack_bf2(bf2f_lo(gv[q][e]) * bf2f_lo(t), bf2f_hi(gv[q][e]) * bf2f_hi(t));
+      }
+      if (i < KB) *reinterpret_cast<u32x4*>(an + i * 16) = nv;
+      an_sum[q] = xv[q];
+      an_norm[q] = nv;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 v = c < C ? *reinterpret_cast<const u32x4*>(an + c * 64 + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+        raw[0][j][4 * i] = v[0];
+        raw[0][j][4 * i + 1] = v[1];
+        raw[0][j][4 * i + 2] = v[2];
+        raw[0][j][4 * i + 3] = v[3];
+      }
+    }
+  }
 
   // --- x paired in unpack order, with sums (per row of x)
   uint32_t xp[MR][J][NP];
@@ -185,6 +278,20 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
     for (int k = lane; k < cnt; k += 64)
       __builtin_amdgcn_raw_buffer_store_b16(f2bf(res[r * p.tile_rows + k]), ry,
                                             (uint32_t)(r * N + gw + k * nwv) * 2, 0, 0);
+  if constexpr (AN) {
+    // the sum and normed rows, from workgroup 0
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    const bool writer = blockIdx.x == 0;
+    const __amdgpu_buffer_rsrc_t rs_out = make_rsrc(p.sum_out, writer ? (uint32_t)p.K * 2 : 0u);
+    const __amdgpu_buffer_rsrc_t rn_out = make_rsrc(p.norm_out, writer ? (uint32_t)p.K * 2 : 0u);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int i = threadIdx.x + 256 * q;
+      const uint32_t o = i < p.K / 8 ? (uint32_t)i * 16 : kOob;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, an_sum[q]), rs_out, o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, an_norm[q]), rn_out, o, 0, 0);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -274,6 +381,26 @@ int qmvp_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
   if ((int64_t)grid_x * c.NW * c.tile_rows < p.N) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: grid too small");
   hipLaunchKernelGGL(fn, dim3(grid_x), dim3(64 * c.NW), c.lds_bytes, stream, p);
   return check_launch("qmvp");
+}
+
+int qmvp_addnorm_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs) {
+  qmvp_fn fn = nullptr;
+  if (bits == 4 && gs == 64 && c.MR == 1 && c.sbw == 16) {
+    if (c.S == 2 && c.U == 3) fn = qmvp_kernel<4, 64, 3, 2, 16, 1, true>;
+    else if (c.S == 2 && c.U == 2) fn = qmvp_kernel<4, 64, 2, 2, 16, 1, true>;
+  }
+  if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmv_addnorm: no fused kernel for this configuration");
+  if (p.M != 1 || p.tiles || p.K / 32 != c.S_inner || !p.r || !p.nw || !p.sum_out || !p.norm_out)
+    return set_error(LISAQ_EINVAL_SHAPE, "qmv_addnorm: launch does not match its configuration");
+  p.chunks = c.S_inner;
+  p.tile_rows = c.tile_rows;
+  if ((int64_t)c.tiles * c.NW * c.tile_rows < p.N) return set_error(LISAQ_EINVAL_SHAPE, "qmvp: grid too small");
+  if (c.NW != 4) return set_error(LISAQ_EINVAL_SHAPE, "qmv_addnorm: four waves per workgroup expected");
+  // + the normed row and the four wave sums
+  const int lds = c.lds_bytes + 2 * p.K + 16;
+  if (int rc = allow_dyn_lds((const void*)fn, lds, "qmvp_addnorm")) return rc;
+  hipLaunchKernelGGL(fn, dim3(c.tiles), dim3(64 * c.NW), lds, stream, p);
+  return check_launch("qmvp_addnorm");
 }
 
 }  // namespace lisaq

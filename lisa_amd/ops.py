@@ -30,6 +30,7 @@ __all__ = [
 
 _ws_lock = threading.Lock()
 _ws: dict = {}
+_ws_retired: list = []
 
 
 def workspace(device: torch.device, nbytes: int, kind: str = "linear") -> torch.Tensor:
@@ -37,12 +38,20 @@ def workspace(device: torch.device, nbytes: int, kind: str = "linear") -> torch.
 
     ``kind`` "linear" is the quantized-matmul workspace (split-K partials of
     the matmul path), reused by calls ordered on one stream; "moe" is scratch
-    for gather_qmm / moe_forward (tile tables, intermediates)."""
+    for gather_qmm / moe_forward (tile tables, intermediates).
+
+    A buffer that is outgrown is replaced but never freed: a HIP graph captured
+    earlier still holds its address in its kernel arguments, and freeing it
+    would let the caching allocator hand that memory to another tensor which a
+    later replay of the graph would then overwrite.  Outgrown buffers stay
+    alive for the life of the process (at most a few per device and kind)."""
     key = (device.type, device.index, kind)
     nbytes = max(int(nbytes), 256)
     with _ws_lock:
         buf = _ws.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                _ws_retired.append(buf)
             buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
             _ws[key] = buf
         return buf

@@ -139,7 +139,8 @@ def qmv_threads(x, w, scales, biases, group_size: int, bits: int, nthreads: int)
 
 def add_rms_norm(x, r, norm_w, eps: float):
     """Prologue of affine_qmv_fast_addnorm (norm_qmv.metal:376-400): s = bf16(x + r);
-    inv = 1/sqrt(sum(s^2)/K + eps) in f32; normed = bf16(norm_w * bf16(s * inv)).  x, r: bf16 bits
+    inv = rsqrt(f32(sum(s^2)/K) + eps) rounded once to f32 (metal::precise::rsqrt, norm_qmv.metal:377);
+    normed = bf16(norm_w * bf16(s * inv)).  x, r: bf16 bits
     [M, K]; norm_w: bf16 bits [K].  Returns (s, normed) as bf16 bits.  The sum of squares is taken
     in float64 (the reference's order is Apple's simd_sum tree, not reproducible here)."""
     x = _c(x, np.uint16)
@@ -148,7 +149,8 @@ def add_rms_norm(x, r, norm_w, eps: float):
     s = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(r))
     sf = bf16_to_f32(s).astype(np.float32)
     ss = (sf.astype(np.float64) ** 2).sum(axis=-1, keepdims=True).astype(np.float32)
-    inv = (np.float32(1.0) / np.sqrt(ss / np.float32(K) + np.float32(eps))).astype(np.float32)
+    a = (ss / np.float32(K) + np.float32(eps)).astype(np.float32)
+    inv = (1.0 / np.sqrt(a.astype(np.float64))).astype(np.float32)
     t = bf16_to_f32(f32_to_bf16(sf * inv)).astype(np.float32)
     normed = f32_to_bf16(bf16_to_f32(_c(norm_w, np.uint16)).reshape(1, K).astype(np.float32) * t)
     return s, normed

@@ -144,3 +144,15 @@ def test_workspace_queries():
     assert lib.lisaq_quantized_matmul_workspace(2048, 5120, 17408, 64, 4) == 0
     assert lib.lisaq_gather_qmm_workspace(32768, 768, 2048, 128, 64, 4) >= 256
     assert lib.lisaq_moe_workspace(4096, 2048, 768, 128, 8, 64, 4) > 32768 * 2048 * 2
+
+
+def test_qmv_addnorm_rejects_overlapping_outputs():
+    """The add+RMSNorm outputs are written while other workgroups still read x and r: an overlap is an
+    error (EINVAL_LAYOUT) found before any device work (the pointers here are never dereferenced)."""
+    lib = _lib.load()
+    K, N = 5120, 17408
+    x, r, nw, w, s, b, so, no, y = (0x100000 * (i + 1) for i in range(9))
+    rc = lib.lisaq_qmv_addnorm(None, x, r, nw, w, s, b, x + 64, no, y, 1, N, K, ctypes.c_float(1e-6), 64, 4, None, 0)
+    assert rc == _lib.EINVAL_LAYOUT and b"overlap" in lib.lisaq_last_error()
+    rc = lib.lisaq_qmv_addnorm(None, x, r, nw, w, s, b, so, r, y, 1, N, K, ctypes.c_float(1e-6), 64, 4, None, 0)
+    assert rc == _lib.EINVAL_LAYOUT

@@ -309,12 +309,13 @@ def test_rejections_raise(dev):
                              to_dev_bf16(b, dev))
 
 
-@pytest.mark.parametrize("N,K", [(264, 5120), (1000, 9728)])
+@pytest.mark.parametrize("N,K", [(264, 5120), (1000, 9728), (17408, 5120), (16384, 4608)])
 def test_qmv_addnorm(dev, oracle, N, K):
     """Residual add + RMSNorm + matvec (jit::affine_qmv_fast_addnorm, matmul.rs:315-443): the sum row
     bit-exact; the normed row within one bf16 step of the oracle (the f32 sum of squares may differ in
     its last bit from the float64 one); y bitwise equal to the matvec on the kernel's own normed row and
-    within tolerance of the oracle's matvec on the oracle's normed row."""
+    within tolerance of the oracle's matvec on the oracle's normed row.  N >= 16384 with K <= 6144 takes the
+    persistent matvec with the add + RMSNorm folded in (one launch); the other shapes the two-launch path."""
     import torch
 
     rng = np.random.default_rng(N + K)
