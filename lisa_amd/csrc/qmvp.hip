@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
       const float total = wave_sum(part[r]);
       // results wait in LDS: a store here would be a vector-memory event
       // between the ring's loads and blur the compiler's exact wait counts
-      if (lane == 0 && k < cnt) res[r * p.tile_rows + k] = total;
+      if (lane == 0) res[r * p.tile_rows + k] = total;
     }
   };
 
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       issue((d + D - 1) % D, k0 + d + D - 1);
-      compute(d, k0 + d);
+      if (k0 + d < cnt) compute(d, k0 + d);  // (uniform: the last step's tail rows are skipped)
     }
   }
   // (a wave's LDS operations complete in order: lane 0's writes are visible)
