@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+CLOCK_WARM_S = 0.03  # sustained load before any timed region (steady shader clock)
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "4-bit qmv GB/s (% HBM peak) @M=1; qmm TFLOP/s (% bf16 MFMA peak) @M=2048"
 
@@ -37,7 +38,7 @@ METRIC = "4-bit qmv GB/s (% HBM peak) @M=1; qmm TFLOP/s (% bf16 MFMA peak) @M=20
 # commands and raw counts).
 QMV_TRAFFIC_BYTES = round((24584.0 * 1.9993 + 136.0) * 1024)
 QMM_TRAFFIC_BYTES = round((223336.7 * 1.9993 + 133386.9) * 1024)
-QMV_KERNEL = "lisaq::qmvp_kernel<4, 64, 3, 2, 16, 1>"
+QMV_KERNEL = "lisaq::qmvp_kernel<4, 64, 3, 2, 16, 1, false>"
 QMM_KERNEL = "lisaq::qmm_kernel<4, 64, 8, 1, 8, true>"  # M=2048: 256-row tiles, last round split over K (+ qmm_hybrid_reduce_kernel)
 
 
@@ -49,9 +50,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--qmm-steps", type=int, default=20)
-    ap.add_argument("--qmm-warmup", type=int, default=10)
     ap.add_argument("--sets", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -116,12 +116,19 @@ def main():
                 step(i)
         return g
 
-    # W untimed warm-up steps, replayed from a graph like the timed ones
+    # W untimed warm-up steps, replayed from a graph like the timed ones, then
+    # replays of the same graph until the GPU has run this load for at least
+    # CLOCK_WARM_S (it reaches its steady clock after ~20 ms of sustained load;
+    # a handful of calls is ~0.1 ms and leaves it ramping)
     g_warm = capture(max(args.warmup, 1))
     g_timed = capture(args.steps)
-    with torch.cuda.stream(stream):
-        g_warm.replay()
-    torch.cuda.synchronize()
+    t_w = time.perf_counter()
+    warm_replays = 0
+    while warm_replays < 1 or time.perf_counter() - t_w < CLOCK_WARM_S:
+        with torch.cuda.stream(stream):
+            g_warm.replay()
+        torch.cuda.synchronize()
+        warm_replays += 1
 
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -138,25 +145,15 @@ def main():
     nbytes = qmv_bytes(M, N, K, bits, gs)
     gbs = nbytes / per_step_s / 1e9
 
-    # --- qmm: prefill M=2048 (eager; each call is ~0.3-1 ms) -------------------
+    # --- qmm: prefill M=2048, timed like the configuration rows (graph replay
+    # after >= CLOCK_WARM_S of replays of the same graph) -------------------------
     Mq = 2048
-    if args.no_qmm:
-        args.qmm_steps = 0
     wq = sets[0]
     xq = torch_x(Mq, K, device=dev, generator=gen)
-    with torch.cuda.stream(stream):
-        for _ in range(args.qmm_warmup if args.qmm_steps else 0):
-            ops.quantized_matmul(xq, *wq, True, gs, bits)
-    torch.cuda.synchronize()
-    q0 = torch.cuda.Event(enable_timing=True)
-    q1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        q0.record(stream)
-        for _ in range(args.qmm_steps):
-            ops.quantized_matmul(xq, *wq, True, gs, bits)
-        q1.record(stream)
-    torch.cuda.synchronize()
-    qmm_s = q0.elapsed_time(q1) * 1e-3 / max(args.qmm_steps, 1)
+    qmm_s = float("nan")
+    if not args.no_qmm:
+        qmm_s = _time_graph(stream, lambda i: ops.quantized_matmul(xq, *wq, True, gs, bits), 1, args.qmm_steps,
+                            warm_s=CLOCK_WARM_S)
     flops = 2.0 * Mq * N * K
     tflops = flops / qmm_s / 1e12
 
@@ -184,7 +181,9 @@ def main():
         "config": {
             "workload": "qmv 4-bit gs64 M=1 K=5120 N=17408 (decode matvec), 8 rotating weight sets",
             "bits": bits, "group_size": gs, "M": M, "K": K, "N": N, "weight_sets": len(sets),
-            "bytes_per_step": nbytes, "timing": "HIP graph replay of the timed steps, hipEvent bracket",
+            "bytes_per_step": nbytes,
+            "timing": f"HIP graph replay of the timed steps, hipEvent bracket, after the W warm-up steps and "
+                      f"{warm_replays} replays of them ({CLOCK_WARM_S * 1e3:.0f} ms of clock warm-up)",
             "wall_s": round(wall, 4),
         },
         "roofline": {
@@ -206,7 +205,7 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def _time_graph(stream, fn, n_sets, steps, warm_s=0.02):
+def _time_graph(stream, fn, n_sets, steps, warm_s=CLOCK_WARM_S):
     """Average seconds per call of fn(i) over `steps` calls replayed from a HIP graph (i cycles
     over n_sets inputs), after untimed replays of the same graph for at least `warm_s` seconds
     (steady clock; the first replays of a new graph over new buffers run slow)."""
@@ -369,7 +368,9 @@ def cpu_baseline(M, N, K, bits, gs, seconds):
     rng = np.random.default_rng(0x5EED)
     w, s, b = np_linear(rng, N, K, bits, gs)
     x = np_x(rng, M, K)
-    threads = min(16, os.cpu_count() or 1)
+    # every core this process may run on (the GPU box grants a share of the host's cores)
+    host_cpus = os.cpu_count() or 1
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host_cpus
     nbytes = qmv_bytes(M, N, K, bits, gs)
 
     def timed(fn, budget, min_calls=1):
@@ -387,6 +388,7 @@ def cpu_baseline(M, N, K, bits, gs, seconds):
     cm, em = timed(lambda: xf @ O.dequantize(w, s, b, gs, bits).T, seconds * 0.2, min_calls=2)
     return {
         "value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "host_cpus": host_cpus, "single_thread_value": round(nbytes * c1 / e1 / 1e9, 3),
         "sample": f"{calls} calls of the same qmv shape (M={M} K={K} N={N} {bits}-bit) in {el:.1f} s on {threads} "
                   f"threads; 1 thread: {nbytes * c1 / e1 / 1e9:.3f} GB/s ({c1} calls); dequantize-then-matmul: "
                   f"{nbytes * cm / em / 1e9:.3f} GB/s ({cm} calls)",
