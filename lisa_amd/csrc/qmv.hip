@@ -443,14 +443,15 @@ QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool sin
     if (f != '3' && qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
     return qmv32_config(M, N, K, gs, bits);
   }
-  // One or two rows with enough rows of W to keep every wave busy: the
-  // persistent kernel; three to eight rows: the one-stream kernel; else one
-  // row: the workgroup dot kernel; otherwise the MFMA streaming kernel.
+  // Two to eight rows: the one-stream kernel (measured at least as fast as
+  // the others at every BASELINE decode shape); one row: the persistent
+  // kernel when there are enough rows of W to keep every wave busy, else the
+  // workgroup dot kernel; otherwise the MFMA streaming kernel.
+  if (!single_pass && M >= 2 && qmvw_supported(M, N, K, gs, bits)) return qmvw_config(M, N, K, gs, bits);
   if (!single_pass && M <= 2 && N >= 16384) {
     const QmvConfig c = qmvp_config(M, N, K, gs, bits);
     if (c.kind == 4) return c;
   }
-  if (!single_pass && M >= 3 && qmvw_supported(M, N, K, gs, bits)) return qmvw_config(M, N, K, gs, bits);
   if (M == 1 && qmvd_supported(M, N, K, gs, bits)) return qmvd_config(M, N, K, gs, bits);
   if (qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits, !single_pass);
   if (qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);

@@ -78,9 +78,14 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
   const int rows = r1 - r0;
   const int units = ((rows + 15) >> 4) * segs;
   const uint32_t rowbytes = (uint32_t)K / 2;
-  const int XS = 2 * K + 16;  // LDS bytes per staged row of x (16-byte pad spreads the banks)
+  // staged row m of x at m * XS + 16 * sig(m): the 16-byte slots (mod 256
+  // bytes) that one step's A reads hit are sig(m) + 4 q for the lane groups
+  // q = 0, 1 (2, 3) reading rows m < 8 -- all distinct with sig(m) = (m & 3)
+  // + 8 (m >> 2), so a half-wave's reads take no bank conflicts
+  const int XS = 2 * K + 256;
+  auto xrow = [&](int m) { return m * XS + 16 * ((m & 3) + 8 * (m >> 2)); };
   unsigned char* ximg = smem;
-  float* sxt = reinterpret_cast<float*>(smem + (MP + 1) * XS);  // [K/64][MP] block sums of x
+  float* sxt = reinterpret_cast<float*>(smem + MP * XS);  // [K/64][MP] block sums of x
   float* part = sxt + (K / 64) * MP;                       // [units][64][RP]
 
   const __amdgpu_buffer_rsrc_t rw =
@@ -125,24 +130,24 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
 
   // --- x into LDS, each 8 codes in unpack order (x0,x4,x1,x5,x2,x6,x3,x7)
   {
-    const int nblk = (MP + 1) * (K / 8);  // 16-byte blocks; rows m >= M (and the zero row MP) read as zero
+    const int nblk = MP * (K / 8);  // 16-byte blocks; rows m >= M read as zero
     for (int i = tid; i < nblk; i += 64 * NW) {
       const int m = i / (K / 8), c = i - m * (K / 8);
       const u32x4 v = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, m < MP ? (uint32_t)(m * K + c * 8) * 2 : kOob, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(m * K + c * 8) * 2, 0, 0));
       u32x4 o;
       o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);  // (x0, x4)
       o[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);  // (x1, x5)
       o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);  // (x2, x6)
       o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);  // (x3, x7)
-      *reinterpret_cast<u32x4*>(ximg + m * XS + c * 16) = o;
+      *reinterpret_cast<u32x4*>(ximg + xrow(m) + c * 16) = o;
     }
   }
   __syncthreads();
   // block sums of x (64 codes), a fixed order per (row, block)
   for (int i = tid; i < MP * (K / 64); i += 64 * NW) {
     const int blk = i / MP, m = i - blk * MP;
-    const u32x4* src = reinterpret_cast<const u32x4*>(ximg + m * XS + blk * 128);
+    const u32x4* src = reinterpret_cast<const u32x4*>(ximg + xrow(m) + blk * 128);
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -165,19 +170,25 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
   qmvdev::PConst kc;
   kc.init();
 
-  // A operands: a lane that carries no x reads the zero row instead (no
-  // branch, so a unit is one straight-line block the compiler can schedule)
-  const unsigned char* abase = (a_on ? ximg + am * XS : ximg + MP * XS) + q * 64;  // + step*256 + i*16
+  // A operands: only lanes that carry x read them (exec-masked LDS reads);
+  // the other lanes keep the zeros written here for the whole launch
+  const unsigned char* abase = ximg + xrow(am) + q * 64;  // + step*256 + i*16
+  u32x4 av[4][4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) av[st][i] = u32x4{0u, 0u, 0u, 0u};
 
   auto compute = [&](int slot, int k) {
     const int u = wave + k * NW;
     const int g = u % segs;
-    u32x4 av[4][4];
+    if (a_on) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
+      for (int st = 0; st < 4; ++st)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        av[st][i] = *reinterpret_cast<const u32x4*>(abase + (4 * g + st) * 256 + i * 16);
+        for (int i = 0; i < 4; ++i)
+          av[st][i] = *reinterpret_cast<const u32x4*>(abase + (4 * g + st) * 256 + i * 16);
+    }
     f32x4w D[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -259,7 +270,7 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
 
 static int qmvw_lds(int MP, int64_t K, int T) {
   const int RP = MP < 4 ? MP : 4;
-  return (int)((MP + 1) * (2 * K + 16) + (K / 64) * MP * 4 + (int64_t)T * (K / 512) * 64 * RP * 4);
+  return (int)(MP * (2 * K + 256) + (K / 64) * MP * 4 + (int64_t)T * (K / 512) * 64 * RP * 4);
 }
 
 QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {

@@ -215,11 +215,11 @@ def test_one_stream_rows_bitwise(dev, oracle, monkeypatch, N, K, gs):
 
 def _one_stream_fits(M, N, K):
     """LDS bytes of the one-stream matvec at its default grid (256 workgroups) within 160 KB: staged
-    rows of x (+ one zero row), block sums, per-unit partials (qmvw.hip, qmvw_lds)."""
+    rows of x (each padded by 256 bytes), block sums, per-unit partials (qmvw.hip, qmvw_lds)."""
     MP = 1 if M == 1 else 2 if M == 2 else 4 if M <= 4 else 8
     RP = min(MP, 4)
     T = (-(-N // 256) + 15) // 16
-    return (MP + 1) * (2 * K + 16) + (K // 64) * MP * 4 + T * (K // 512) * 64 * RP * 4 <= 160 * 1024
+    return MP * (2 * K + 256) + (K // 64) * MP * 4 + T * (K // 512) * 64 * RP * 4 <= 160 * 1024
 
 
 @pytest.mark.parametrize("bits", [2, 4])
