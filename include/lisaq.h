@@ -175,6 +175,24 @@ LISAQ_API size_t lisaq_gather_qmm_workspace(int64_t R, int64_t N, int64_t K, int
 /* act = bf16(silu(gate)) * up in bf16 (EM:413, core/norm.rs bf16_silu). */
 LISAQ_API int lisaq_swiglu(void* stream, const void* gate, const void* up, void* act, int64_t n);
 
+/* SwiGLU of the gate and up gather_qmm over expert-sorted rows, in one launch
+ * (EM:373-413: gather_qmm(x_sorted, gate), gather_qmm(x_sorted, up),
+ * bf16_silu(gate) * up).  Row r of the sorted input is x[x_rows[r]] (x [T,H]
+ * bf16; x_rows int32 [R], entries clamped to [0, T)), so no gathered copy of x
+ * is made; rhs_indices int32 [R] sorted expert ids; gate/up stacks
+ * [E,I,H*bits/32] (+ scales/biases [E,I,H/gs]); act [R,I] bf16, 16-byte aligned.
+ * Every run, whatever its length, uses the matmul arithmetic (bf16 weights,
+ * f32 accumulation, gate and up each rounded to bf16 before the SwiGLU); a run
+ * of at least qmv_batch_limit(H, I) rows is bitwise equal to gather_qmm +
+ * gather_qmm + swiglu.  H % 64 == 0, I % 8 == 0.
+ * workspace: lisaq_gather_qmm_swiglu_workspace() bytes. */
+LISAQ_API int lisaq_gather_qmm_swiglu(void* stream, const void* x, const int32_t* x_rows,
+                                      const int32_t* rhs_indices, const uint32_t* gate_w, const void* gate_s,
+                                      const void* gate_b, const uint32_t* up_w, const void* up_s,
+                                      const void* up_b, void* act, int64_t R, int64_t T, int64_t I, int64_t H,
+                                      int E, int group_size, int bits, void* workspace, size_t workspace_bytes);
+LISAQ_API size_t lisaq_gather_qmm_swiglu_workspace(int64_t R, int64_t I, int E);
+
 /* Sorted combine (KM:38-119, moe_combine.metal): out[t,d] (bf16) =
  * bf16( colsum_small<k>( f32(down_sorted[inverse[t*k+j], d]) * w[t*k+j] ) ).
  * Bit-exact with the reference summation order.  1 <= k <= 32. */
@@ -191,7 +209,10 @@ LISAQ_API int lisaq_moe_combine(void* stream, const void* down_sorted, const flo
  * moe.rs:263-332, 415-420) take the fused decode path of moe_decode.rs
  * (routing + gate|up + SwiGLU, then down + combine: two launches),
  * with the same rounding points; the environment variable LISAQ_MOE_FUSED=0
- * selects the generic path instead.
+ * selects the generic path instead.  Many tokens (T*k >= 32*E, H % 64 == 0,
+ * I % 64 == 0) take lisaq_gather_qmm_swiglu for gate|up + SwiGLU (one launch,
+ * x read through the sort's row map); LISAQ_MOE_GU=0 selects the three-step
+ * gather, gate, up, SwiGLU sequence instead.
  * workspace: lisaq_moe_workspace() bytes, zero-filled before first use. */
 LISAQ_API int lisaq_moe_forward(void* stream, const void* x, const float* logits, const uint32_t* gate_w,
                       const void* gate_s, const void* gate_b, const uint32_t* up_w,

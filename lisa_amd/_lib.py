@@ -60,6 +60,8 @@ SIGNATURES = {
     "lisaq_gather_qmm": (ci, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci, ci, vp, sz]),
     "lisaq_gather_qmm_workspace": (sz, [i64, i64, i64, ci, ci, ci]),
     "lisaq_swiglu": (ci, [vp, vp, vp, vp, i64]),
+    "lisaq_gather_qmm_swiglu": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ci, ci, ci, vp, sz]),
+    "lisaq_gather_qmm_swiglu_workspace": (sz, [i64, i64, ci]),
     "lisaq_moe_decode_supported": (ci, [i64, i64, i64, ci, ci, ci, ci]),
     "lisaq_moe_combine": (ci, [vp, vp, vp, vp, vp, i64, ci, i64]),
     "lisaq_moe_forward": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,

@@ -175,6 +175,13 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   if (L.Mmax < 1) L.Mmax = 1;
   L.qc = qmv_config(L.Mmax, N, K, gs, bits, /*single_pass=*/true);
   L.mc = qmm_config(L.limit, N, K, gs, bits);
+  {
+    const int mt = tune_int("LISAQ_GATHER_MT", L.mc.MT);
+    if (mt == 4 || mt == 6 || mt == 8) {
+      L.mc.MT = mt;
+      L.mc.BM = 32 * mt;
+    }
+  }
   L.qmv_cap = (int)(runs * ((N + L.qc.tile_rows - 1) / L.qc.tile_rows));
   L.qmm_cap = (mr >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
   L.qmv_off = 256;
@@ -547,6 +554,60 @@ int lisaq_gather_rows(void* stream, const void* x, const int32_t* rows, void* ou
   return launch_gather_rows((hipStream_t)stream, (const uint16_t*)x, rows, (uint16_t*)out, R, H);
 }
 
+}  // extern "C"
+
+// gate|up tiles of the MoE prefill: every run in 128-row tiles of 128 columns
+static int64_t gu_cap(int64_t R, int64_t I, int E) {
+  const int64_t runs = R < E ? R : E;
+  return ((R + kGuBM - 1) / kGuBM + runs) * ((I + kGuBN - 1) / kGuBN);
+}
+
+// The fused gate|up matmul serves the prefill when the average expert run is
+// at least 32 rows (short runs then cost one 32-row block of matrix work each).
+static bool moe_gu_path(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
+  const int64_t R = T * k;
+  return path_int("LISAQ_MOE_GU", 1) != 0 && R >= 32 * (int64_t)E && H % 64 == 0 && I % 64 == 0 &&
+         (bits == 4 || bits == 2) && (gs == 32 || gs == 64 || gs == 128) && T * H < ((int64_t)1 << 31);
+}
+
+// Gate|up + SwiGLU over sorted rows: tile table (from the expert offsets
+// when the caller has them, else from the sorted ids), then one matmul launch.
+static int gate_up_swiglu(hipStream_t st, const void* x, const int32_t* xrows, int64_t T, const int32_t* sorted,
+                          const int32_t* offs, const uint32_t* gw, const void* gsc, const void* gbi,
+                          const uint32_t* uw, const void* usc, const void* ubi, void* act, int64_t R, int64_t I,
+                          int64_t H, int E, int gs, int bits, void* ws, size_t ws_bytes) {
+  const int64_t cap = gu_cap(R, I, E);
+  LISAQ_REQUIRE(ws != nullptr && 256 + (size_t)cap * 16 <= ws_bytes && aligned(ws, 256), LISAQ_EWORKSPACE,
+                "gate|up: 256-byte aligned workspace of %zu bytes required (got %zu)", 256 + (size_t)cap * 16,
+                ws_bytes);
+  LISAQ_REQUIRE(T > 0 && T * H < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "gate|up: x larger than 2^31 elements");
+  LISAQ_REQUIRE(aligned(act, 16), LISAQ_EINVAL_LAYOUT, "gate|up: act must be 16-byte aligned");
+  char* gb = (char*)ws;
+  if (int rc = launch_tile_table(st, sorted, offs, R, E, (int)I, /*limit=*/1, 16, kGuBM, kGuBN, nullptr, 0,
+                                 (int4*)(gb + 256), (int)cap, (int32_t*)gb))
+    return rc;
+  QmmParams p{};
+  p.x = (const uint16_t*)x;
+  p.w = gw;
+  p.s = (const uint16_t*)gsc;
+  p.b = (const uint16_t*)gbi;
+  p.w2 = uw;
+  p.s2 = (const uint16_t*)usc;
+  p.b2 = (const uint16_t*)ubi;
+  p.xrows = xrows;
+  p.xrows_max = (int)(T - 1);
+  p.y = (uint16_t*)act;
+  p.tiles = (const int4*)(gb + 256);
+  p.M = (int)R;
+  p.N = (int)I;
+  p.K = (int)H;
+  p.G = (int)(H / gs);
+  p.ksplit = 1;
+  return qmm_gu_launch(st, p, bits, gs, (int)cap);
+}
+
+extern "C" {
+
 size_t lisaq_gather_qmm_workspace(int64_t R, int64_t N, int64_t K, int E, int gs, int bits) {
   if (R <= 0 || N <= 0 || K <= 0 || E <= 0 || gs <= 0 || K % gs) return 256;
   return gather_layout(R, N, K, E, gs, bits).total;
@@ -580,6 +641,31 @@ int lisaq_swiglu(void* stream, const void* gate, const void* up, void* act, int6
   if (n == 0) return LISAQ_OK;
   LISAQ_REQUIRE(gate && up && act, LISAQ_EINVAL_LAYOUT, "swiglu: null tensor pointer");
   return launch_swiglu((hipStream_t)stream, (const uint16_t*)gate, (const uint16_t*)up, (uint16_t*)act, n);
+}
+
+size_t lisaq_gather_qmm_swiglu_workspace(int64_t R, int64_t I, int E) {
+  if (R <= 0 || I <= 0 || E <= 0) return 256;
+  return 256 + up256((size_t)gu_cap(R, I, E) * 16);
+}
+
+int lisaq_gather_qmm_swiglu(void* stream, const void* x, const int32_t* x_rows, const int32_t* rhs_indices,
+                            const uint32_t* gw, const void* gsc, const void* gbi, const uint32_t* uw,
+                            const void* usc, const void* ubi, void* act, int64_t R, int64_t T, int64_t I, int64_t H,
+                            int E, int gs, int bits, void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(R >= 0 && T >= 0 && I > 0 && H > 0 && E >= 1, LISAQ_EINVAL_SHAPE, "gather_qmm_swiglu: bad sizes");
+  if (R == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(T > 0, LISAQ_EINVAL_SHAPE, "gather_qmm_swiglu: rows of x required");
+  LISAQ_REQUIRE(R <= (1 << 24), LISAQ_EINVAL_SHAPE, "gather_qmm_swiglu: R=%lld too large", (long long)R);
+  LISAQ_REQUIRE(x_rows && rhs_indices, LISAQ_EINVAL_LAYOUT, "gather_qmm_swiglu: null index pointer");
+  int rc;
+  if ((rc = validate_mm("gather_qmm_swiglu gate", x, gw, gsc, gbi, act, T, I, H, 1, gs, bits))) return rc;
+  if ((rc = validate_mm("gather_qmm_swiglu up", x, uw, usc, ubi, act, T, I, H, 1, gs, bits))) return rc;
+  LISAQ_REQUIRE(H % 64 == 0 && I % 8 == 0, LISAQ_EUNSUPPORTED,
+                "gather_qmm_swiglu: need H %% 64 == 0 and I %% 8 == 0 (H=%lld, I=%lld)", (long long)H, (long long)I);
+  LISAQ_REQUIRE(E <= kTileTableMaxExperts, LISAQ_EUNSUPPORTED, "gather_qmm_swiglu: E=%d experts", E);
+  return gate_up_swiglu((hipStream_t)stream, x, x_rows, T, rhs_indices, nullptr, gw, gsc, gbi, uw, usc, ubi, act,
+                        R, I, H, E, gs, bits, ws, ws_bytes);
 }
 
 int lisaq_moe_combine(void* stream, const void* down, const float* wts, const int32_t* inv, void* out, int64_t T,
@@ -622,7 +708,8 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
   // rows (a token picks an expert once)
   const size_t g1 = gather_layout(R, I, H, E, gs, bits, T).total;
   const size_t g2 = gather_layout(R, H, I, E, gs, bits, T).total;
-  L.gws = take(g1 > g2 ? g1 : g2);
+  const size_t g3 = 256 + up256((size_t)gu_cap(R, I, E) * 16);
+  L.gws = take(g1 > g2 ? (g1 > g3 ? g1 : g3) : (g2 > g3 ? g2 : g3));
   L.total = o;
   return L;
 }
@@ -675,6 +762,21 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   LISAQ_REQUIRE(E <= 1024, LISAQ_EINVAL_SHAPE, "moe_forward: need E <= 1024 (E=%d)", E);
   if ((rc = launch_sort_parallel(st, idx, R, E, k, sorted, order, rows, inv, offs, (int32_t*)(B + L.hist))))
     return rc;
+  if (moe_gu_path(T, H, I, E, k, gs, bits)) {
+    // gate|up + SwiGLU in one matmul launch reading x through the row map,
+    // then the down gather and the combine
+    if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
+    if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
+    if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, d, R, H, I, 1, gs, bits))) return rc;
+    if ((rc = gate_up_swiglu(st, x, rows, T, sorted, offs, gw, gsc, gbi, uw, usc, ubi, g, R, I, H, E, gs, bits, gws,
+                             gws_bytes)))
+      return rc;
+    const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T);
+    LISAQ_REQUIRE(DN.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
+    if ((rc = gather_tables(st, DN, sorted, R, H, E, gws, offs))) return rc;
+    if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;
+    return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
+  }
   if ((rc = lisaq_gather_rows(st, x, rows, xs, R, H))) return rc;
   // gate and up share one set of tile tables; every run is at most T rows
   if ((rc = validate_mm("moe_forward gate", xs, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;

@@ -15,6 +15,13 @@ struct QmmParams {
   float* partial;       // split over K: [ksplit, M, N] f32 partial sums (plain launches only)
   int ksplit;           // K splits (1: the kernel writes y)
   int full_tiles;       // split launches: whole tiles before the split units (0: every tile split)
+  // gate|up launches (qmm_gu_launch): the up stack, and the x row of each
+  // tile row (x row t.y + r of a tile is x[xrows[t.y + r]])
+  const uint32_t* w2;
+  const uint16_t* s2;
+  const uint16_t* b2;
+  const int32_t* xrows;
+  int xrows_max;  // rows of x - 1 (row map entries are clamped to [0, xrows_max])
 };
 
 struct QmmConfig {
@@ -30,5 +37,11 @@ QmmConfig qmm_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool all
 // the partials, or runs unsplit when ws is missing or too small.
 int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, int gs, int grid_x,
                int grid_y, void* ws = nullptr, size_t ws_bytes = 0);
+
+// Gate|up matmul of the MoE prefill: tile-table launch of `grid` workgroups,
+// y = SwiGLU(x . gate^T, x . up^T) over 128-column output tiles of 128 rows,
+// x rows gathered through p.xrows (qmm_gu.hip).
+int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid);
+constexpr int kGuBM = 128, kGuBN = 128;  // row / output-column tile of qmm_gu_launch
 
 }  // namespace lisaq

@@ -1,0 +1,36 @@
+// Gate|up matmul of the MoE prefill (the qmm kernel with GU = true): one
+// launch computes both expert projections of each 128-row x 128-column tile,
+// reads the tile's x rows through the sort's row map, and writes SwiGLU of the
+// two -- the reference's gather_qmm(gate), gather_qmm(up), swiglu sequence
+// (crates/lisa-engine/src/models/qwen4/moe.rs:373-413) with the same bits as those
+// three steps over matmul tiles.
+#include "qmm_kernel.h"
+
+namespace lisaq {
+
+int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid) {
+  constexpr int MT = kGuBM / 32;
+  static_assert(kGuBN == QmmLds<4, 64, MT, 1, 8>::BN / 2, "gate|up output tile");
+  LISAQ_REQUIRE(p.tiles && p.xrows && p.w2 && p.s2 && p.b2, LISAQ_EINVAL_LAYOUT, "qmm_gu: missing table or stack");
+  LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
+  qmm_fn fn = nullptr;
+  auto pick = [&](auto bt) {
+    constexpr int B = decltype(bt)::value;
+    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, true>;
+    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, true>;
+    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, true>;
+  };
+  if (bits == 4) pick(std::integral_constant<int, 4>{});
+  if (bits == 2) pick(std::integral_constant<int, 2>{});
+  if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm_gu: bits=%d group_size=%d not supported", bits, gs);
+  // the 4-bit ring's size at either code width: the epilogue's gate|up
+  // exchange needs that much
+  constexpr int lds = QmmLds<4, 64, MT, 1, 8>::TOTAL;
+  static_assert(lds >= QmmLds<2, 64, MT, 1, 8>::TOTAL, "ring size");
+  if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm_gu")) return rc;
+  if (grid <= 0) return LISAQ_OK;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(512), lds, stream, p);
+  return check_launch("qmm_gu");
+}
+
+}  // namespace lisaq

@@ -21,6 +21,7 @@
 #pragma once
 #include "lisaq_common.h"
 #include "qmm.h"
+#include "moe_dev.h"
 #include <type_traits>
 #include <utility>
 
@@ -159,7 +160,15 @@ struct QmmLds {
 // SIMD, NT = 1, 128 accumulator registers: a SIMD's second wave fills the
 // matrix-core bubbles of the first).  Either way every W element is
 // dequantized once per workgroup.
-template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT>
+//
+// GU (gate|up, tile-table launches only): LDS tile rows 0..BN/2-1 are gate
+// rows nt0.., rows BN/2.. the up rows with the same indices, so the waves of
+// the first half hold x . gate^T and the second half x . up^T for the same
+// BN/2 output columns; the epilogue exchanges them through LDS and writes
+// SwiGLU(bf16 gate, bf16 up) (the arithmetic of moe_dev.h).  x rows are read
+// through p.xrows (no gathered copy of x), and 32-row blocks past the tile's
+// rows skip their matrix instructions (short expert runs).
+template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT, bool GU = false>
 __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
   using L = QmmLds<BITS, GS, MT, NT, WN>;
@@ -179,21 +188,32 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   const uint16_t* bi = p.b;
   const uint16_t* x = p.x;
   uint16_t* y = p.y;
+  const uint32_t* w2 = p.w2;
+  const uint16_t* sc2 = p.s2;
+  const uint16_t* bi2 = p.b2;
   int M = p.M;
-  int m0, nt0, split = 0, ksplit = p.ksplit, unit = -1;
+  int m0, nt0, split = 0, ksplit = p.ksplit, unit = -1, trow = 0;
   bool whole = !SPLIT;  // (plain launches: every workgroup a whole tile)
-  if (p.tiles) {
+  static_assert(!GU || (!SPLIT && BN % 128 == 0), "gate|up tiles");
+  if (GU || p.tiles) {
     const int4 t = p.tiles[blockIdx.x];
     if (t.x < 0) return;
     const int64_t e = t.x;
     w += e * (int64_t)p.N * (p.K / G::PACK);
     sc += e * (int64_t)p.N * p.G;
     bi += e * (int64_t)p.N * p.G;
-    x += (int64_t)t.y * p.K;
+    if constexpr (GU) {
+      w2 += e * (int64_t)p.N * (p.K / G::PACK);
+      sc2 += e * (int64_t)p.N * p.G;
+      bi2 += e * (int64_t)p.N * p.G;
+      trow = t.y;
+    } else {
+      x += (int64_t)t.y * p.K;
+    }
     y += (int64_t)t.y * p.N;
     M = t.z;
     m0 = 0;
-    nt0 = t.w * BN;
+    nt0 = t.w * (GU ? BN / 2 : BN);
   } else {
     // row-block major: consecutive workgroups share an x row block and walk W.
     // Split launches: either every tile split over K (split s of every tile
@@ -221,6 +241,10 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
     m0 = (tile / gn) * BM;
   }
 
+  // 32-row blocks of this tile that hold rows (the rest are clamped copies of
+  // the last row and never stored): their matrix instructions are skipped
+  const int mact = GU ? __builtin_amdgcn_readfirstlane(M - m0 >= BM ? MT : (M - m0 + 31) >> 5) : MT;
+
   // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
   // matrix are clamped to the last one, their results are never stored)
   // x: BM/8 instructions of 1 KB, XI per wave; lane l fills row 8g + l/8,
@@ -231,9 +255,22 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   // that x fits 2^31 elements)
   const int xrow0 = m0 + wave * XI * 8 + (lane >> 3);
   const uint32_t xchunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 3);
+  uint32_t xsrc[GU ? XI : 1];  // GU: element offset of each copy's gathered x row
+  if constexpr (GU) {
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+      const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
+      const int xr = p.xrows[trow + row];
+      xsrc[i] = (uint32_t)(xr < 0 ? 0 : xr > p.xrows_max ? p.xrows_max : xr) * (uint32_t)p.K;
+    }
+  }
   auto xoff = [&](int i) -> uint32_t {
-    const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
-    return (uint32_t)row * (uint32_t)p.K + (xchunk ^ (((wave * XI + i) & 1) << 3));
+    if constexpr (GU) {
+      return xsrc[i] + (xchunk ^ (((wave * XI + i) & 1) << 3));
+    } else {
+      const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
+      return (uint32_t)row * (uint32_t)p.K + (xchunk ^ (((wave * XI + i) & 1) << 3));
+    }
   };
   // W: BN rows x RB bytes, row-major; 16 bytes per lane: WB bytes per wave in
   // WI instructions (the last lanes idle when a wave's share is under 1 KB)
@@ -246,12 +283,18 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
     const int off = wave * WB + i * 1024 + lane * 16;  // byte in the W tile
-    int n = nt0 + off / L::RB;
+    int rr = off / L::RB;
+    const uint32_t* wb = w;
+    if (GU && rr >= BN / 2) {
+      wb = w2;
+      rr -= BN / 2;
+    }
+    int n = nt0 + rr;
     n = n < p.N ? n : p.N - 1;
     // 4-bit: physical half (off / 16) % 2 of tile row off / 32 holds logical
     // half ^ w_swz(row)
     const int lb = BITS == 4 ? (off % L::RB) ^ (w_swz(off / L::RB) << 4) : off % L::RB;
-    wsrc[i] = reinterpret_cast<const unsigned char*>(w) + n * rowbytes + lb;
+    wsrc[i] = reinterpret_cast<const unsigned char*>(wb) + n * rowbytes + lb;
   }
   // scales / biases: per row the 4-byte-aligned bf16 pair holding the step's
   // group(s); 64 rows per instruction (BN/64 instructions per array, spread
@@ -280,9 +323,19 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
     const int idx = wave + NWV * (q - WI);  // 0 .. 2*SI-1: s row blocks, then b row blocks
     const bool is_b = idx >= SI;
     const int blk = is_b ? idx - SI : idx;
-    // (lanes of this instruction load rows blk*64 + lane)
-    const int64_t roff = (int64_t)(nt0 + blk * 64 + lane < p.N ? nt0 + blk * 64 + lane : p.N - 1) * p.G + g;
-    const uint16_t* src = (is_b ? bi : sc) + (roff & ~(int64_t)1);  // (G is even: 4-byte aligned)
+    // (lanes of this instruction load tile rows blk*64 + lane; GU: the second
+    // half of the blocks from the up stack)
+    const bool up = GU && blk >= SI / 2;
+    const int nb = nt0 + (up ? blk - SI / 2 : blk) * 64 + lane;
+    const int64_t roff = (int64_t)(nb < p.N ? nb : p.N - 1) * p.G + g;
+    // (the stack by wave-uniform arithmetic: a select over four pointers
+    // becomes a lookup table in scratch memory)
+    uintptr_t base = reinterpret_cast<uintptr_t>(is_b ? bi : sc);
+    if constexpr (GU)
+      base += up ? (is_b ? reinterpret_cast<uintptr_t>(bi2) - reinterpret_cast<uintptr_t>(bi)
+                         : reinterpret_cast<uintptr_t>(sc2) - reinterpret_cast<uintptr_t>(sc))
+                 : 0;
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(base) + (roff & ~(int64_t)1);  // (G is even: 4-byte aligned)
     load_lds4(src, st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
   };
   auto issue_w = [&](int k, int stage) {
@@ -304,7 +357,8 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
       const int r = (wn * NT + nt) * 32 + col;
       // half of the staged pair: the lane's group (gs 32: the step's two
       // groups, pair-aligned since G is even; else the element's parity)
-      const int n = nt0 + r < p.N ? nt0 + r : p.N - 1;
+      const int rn = GU ? r % (BN / 2) : r;
+      const int n = nt0 + rn < p.N ? nt0 + rn : p.N - 1;
       const int half = GS == 32 ? h : (int)(((int64_t)n * p.G + g0) & 1);
       const int si = r * 4 + half * 2;
       o.s[nt] = *reinterpret_cast<const uint16_t*>(st + L::W + si);
@@ -405,7 +459,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
       }
       // matrix instruction (issued before the slot's LDS reads, so its operand
       // wait does not also wait for them)
-      {
+      if (!GU || mt == 0 || mt < mact) {
         const u32x4 aw = (j & 1) ? a1[mt] : a0[mt];
         const u32x4 bw = u32x4{bcur[nt][4 * j], bcur[nt][4 * j + 1], bcur[nt][4 * j + 2], bcur[nt][4 * j + 3]};
         // W as the row operand, x as the column operand: the accumulator is
@@ -480,6 +534,52 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   // (f32 split partial) store each when N % 4 == 0.  A split writes its f32
   // partial instead (one uniform branch around the whole store loop keeps the
   // accumulators in registers).
+  if constexpr (GU) {
+    // exchange through LDS (after every copy into the ring has landed and
+    // every wave is past its last read): [2][BM][BN/2 + 8] bf16, gate rows
+    // then up rows, 16 bytes of padding per row against bank conflicts
+    constexpr int HN = BN / 2, XS = HN + 8;
+    // (launched with the 4-bit ring's LDS size at either code width)
+    static_assert(2 * BM * XS * 2 <= QmmLds<4, GS, MT, NT, WN>::TOTAL, "gate|up exchange fits the ring");
+    wait_vm<0>();
+    wait_lgkm0();
+    block_sync();
+    uint16_t* ex = reinterpret_cast<uint16_t*>(smem);
+    const int half = wn / (WN / 2), wc = wn % (WN / 2);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x16& a = acc[mt][nt];
+          const int c = (wc * NT + nt) * 32 + 8 * g + 4 * h;
+          *reinterpret_cast<u32x2*>(ex + (half * BM + mt * 32 + col) * XS + c) =
+              u32x2{pk_bf16(a[4 * g], a[4 * g + 1]), pk_bf16(a[4 * g + 2], a[4 * g + 3])};
+        }
+    wait_lgkm0();
+    block_sync();
+    // 8 outputs per thread and pass; N % 8 == 0 (host)
+    constexpr int CH = HN / 8, PASSES = BM * CH / (64 * WN);
+    static_assert(BM * CH % (64 * WN) == 0, "exchange passes");
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int c = ps * 64 * WN + (int)threadIdx.x;
+      const int r = c / CH, cc = (c % CH) * 8;
+      if (r >= M || nt0 + cc >= p.N) continue;
+      const u32x4 gv = *reinterpret_cast<const u32x4*>(ex + r * XS + cc);
+      const u32x4 uv = *reinterpret_cast<const u32x4*>(ex + (BM + r) * XS + cc);
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = swiglu_bf16(bf2f_lo(gv[j]), bf2f_lo(uv[j]));
+        const uint32_t hi = swiglu_bf16(bf2f_hi(gv[j]), bf2f_hi(uv[j]));
+        o[j] = lo | (hi << 16);
+      }
+      *reinterpret_cast<u32x4*>(y + (int64_t)r * p.N + nt0 + cc) = o;
+    }
+    return;
+  }
   const bool vec = (p.N & 3) == 0;
   auto store = [&](auto put4, auto put1) {
 #pragma unroll

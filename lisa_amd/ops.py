@@ -24,7 +24,7 @@ from ._lib import LisaqError
 
 __all__ = [
     "LisaqError", "quantized_matmul", "quantized_matmul_serial_rows", "qmv", "qmm", "gather_qmm",
-    "dequantize", "quantize", "moe_route", "moe_sort", "gather_rows", "swiglu", "moe_combine",
+    "dequantize", "quantize", "moe_route", "moe_sort", "gather_rows", "swiglu", "gather_qmm_swiglu", "moe_combine",
     "moe_forward", "qmv_batch_limit", "detect_group_size",
 ]
 
@@ -280,6 +280,35 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     out = torch.empty_like(gate)
     _lib.call("lisaq_swiglu", _stream(gate), gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel())
     return out
+
+
+def gather_qmm_swiglu(x, x_rows, gate, up, rhs_indices, group_size=64, bits=4) -> torch.Tensor:
+    """SwiGLU of the gate and up ``gather_qmm`` over expert-sorted rows in one launch (moe.rs:373-413):
+    row r is ``x[x_rows[r]]`` (``x`` ``[T, H]``), ``rhs_indices`` ``[R]`` sorted expert ids, ``gate`` /
+    ``up`` ``(w, scales, biases)`` stacks ``[E, I, H*bits/32]`` -> act ``[R, I]``.  Every run uses the
+    matmul arithmetic (runs of at least ``qmv_batch_limit(H, I)`` rows are bitwise equal to
+    ``swiglu(gather_qmm(gate), gather_qmm(up))``)."""
+    x = _bf16(x, "x")
+    rows = x_rows.to(torch.int32).contiguous()
+    rhs = rhs_indices.to(torch.int32).contiguous()
+    gw, gsc, gbi = _u32(gate[0], "gate w"), _bf16(gate[1], "gate scales"), _bf16(gate[2], "gate biases")
+    uw, usc, ubi = _u32(up[0], "up w"), _bf16(up[1], "up scales"), _bf16(up[2], "up biases")
+    _require(x.dim() == 2, _lib.EINVAL_SHAPE, f"gather_qmm_swiglu: x {tuple(x.shape)} must be [T, H]")
+    T, H = x.shape
+    R = rows.numel()
+    _require(rhs.numel() == R, _lib.EINVAL_SHAPE, f"gather_qmm_swiglu: {rhs.numel()} indices for {R} rows")
+    _require(gw.dim() == 3 and gw.shape[2] * 32 // bits == H and uw.shape == gw.shape, _lib.EINVAL_SHAPE,
+             f"gather_qmm_swiglu: gate {tuple(gw.shape)} / up {tuple(uw.shape)} do not match H={H}, bits={bits}")
+    E, I = gw.shape[0], gw.shape[1]
+    for t in (gsc, gbi, usc, ubi):
+        _require(t.shape == (E, I, H // group_size), _lib.EINVAL_SHAPE, "gather_qmm_swiglu: scales/biases shape mismatch")
+    act = torch.empty(R, I, dtype=torch.bfloat16, device=x.device)
+    nbytes = _lib.load().lisaq_gather_qmm_swiglu_workspace(R, I, E)
+    ws = workspace(x.device, nbytes, "moe")
+    _lib.call("lisaq_gather_qmm_swiglu", _stream(x), x.data_ptr(), rows.data_ptr(), rhs.data_ptr(), gw.data_ptr(),
+              gsc.data_ptr(), gbi.data_ptr(), uw.data_ptr(), usc.data_ptr(), ubi.data_ptr(), act.data_ptr(), R, T,
+              I, H, E, group_size, bits, ws.data_ptr(), ws.numel())
+    return act
 
 
 def moe_combine(down_sorted, weights, inverse, T: int, k: int) -> torch.Tensor:

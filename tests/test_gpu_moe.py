@@ -270,3 +270,63 @@ def test_moe_forward_generic_equals_composition(dev, monkeypatch):
     d = ops.gather_qmm(ops.swiglu(g, u), *dv[2], rhs_indices=srt)
     ref = ops.moe_combine(d, rw.reshape(-1), inv, T, k)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("T,E,k,H,I,bits,gs", [(512, 16, 4, 512, 320, 4, 64), (300, 8, 2, 256, 192, 2, 32),
+                                             (1024, 32, 8, 1024, 768, 4, 128), (640, 16, 2, 128, 64, 4, 64)])
+def test_gather_qmm_swiglu(dev, oracle, monkeypatch, T, E, k, H, I, bits, gs):
+    """The fused gate|up + SwiGLU matmul (x rows read through the sort's row
+    map) with skewed routing, so that long runs and a run shorter than the
+    matvec limit (5 rows) occur: runs at or above the limit bitwise equal to
+    swiglu(gather_qmm(gate), gather_qmm(up)) on the gathered rows (the same
+    matmul arithmetic); the short run against the oracle's matmul arithmetic
+    (gate and up rounded to bf16, then the bf16 SwiGLU: two roundings deep,
+    so the bound is 2e-2 + 2e-2|ref|); and moe_forward, which takes this path
+    for T*k >= 32*E, bitwise equal to its steps composed from the public entry
+    points (route, sort, gather_qmm_swiglu, gather_qmm(down), combine) and
+    identical in routing to the three-step path (LISAQ_MOE_GU=0)."""
+    import torch
+
+    rng = np.random.default_rng(T + 7 * E + bits)
+    stk = lambda n, kk: tuple(a.reshape(E, n, -1) for a in np_linear(rng, E * n, kk, bits, gs))
+    G, U, D = stk(I, H), stk(I, H), stk(H, I)
+    x = np_x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[:, 0] += 2.5  # a popular expert
+    lg[:, E - 1] = -50.0  # a rare one: picked by 5 tokens only
+    lg[:5, E - 1] = 50.0
+    dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
+    xd, lgd = to_dev_bf16(x, dev), to_dev(lg, dev)
+    ridx, rw = ops.moe_route(lgd, k)
+    srt, order, rows, inv, offs = ops.moe_sort(ridx.reshape(-1), E, k)
+    act = ops.gather_qmm_swiglu(xd, rows, dv[0], dv[1], srt, gs, bits)
+    xs = ops.gather_rows(xd, rows)
+    comp = ops.swiglu(ops.gather_qmm(xs, *dv[0], rhs_indices=srt, group_size=gs, bits=bits),
+                      ops.gather_qmm(xs, *dv[1], rhs_indices=srt, group_size=gs, bits=bits))
+    a_h, c_h, offs_h, rows_h = from_dev_bf16(act), from_dev_bf16(comp), offs.cpu().numpy(), rows.cpu().numpy()
+    sizes = np.diff(offs_h)
+    lim = ops.qmv_batch_limit(H, I)
+    assert sizes.max() >= lim and sizes[E - 1] == 5, sizes
+    for e in range(E):
+        a, b = offs_h[e], offs_h[e + 1]
+        if b - a >= lim:
+            assert np.array_equal(a_h[a:b], c_h[a:b]), f"expert {e} ({b - a} rows)"
+        elif b > a:
+            xr = x[rows_h[a:b]]
+            g = oracle.f32_to_bf16(oracle.qmm(xr, G[0][e], G[1][e], G[2][e], gs, bits))
+            u = oracle.f32_to_bf16(oracle.qmm(xr, U[0][e], U[1][e], U[2][e], gs, bits))
+            ref = bf16_bits_to_f32(oracle.swiglu(g, u))
+            assert_close_bf16(a_h[a:b], ref, rtol=2e-2, what=f"short run of expert {e} ({b - a} rows)")
+    # the whole block: fused path bitwise equal to its composition; routing as the three-step path
+    assert T * k >= 32 * E and H % 64 == 0 and I % 64 == 0
+    out, idx, w = ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, gs, bits, return_routing=True)
+    d = ops.gather_qmm(act, *dv[2], rhs_indices=srt, group_size=gs, bits=bits)
+    ref = ops.moe_combine(d, rw.reshape(-1), inv, T, k)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    monkeypatch.setenv("LISAQ_MOE_GU", "0")
+    out0, idx0, w0 = ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, gs, bits, return_routing=True)
+    assert torch.equal(idx, idx0) and torch.equal(w, w0)
+    long_tok = np.all(sizes[idx.cpu().numpy()] >= lim, axis=1)
+    assert long_tok.any()
+    assert np.array_equal(from_dev_bf16(out)[long_tok], from_dev_bf16(out0)[long_tok])
+    torch.cuda.synchronize()
