@@ -61,6 +61,8 @@ def main():
                     help="only run a plain 64 MiB device copy (the reference kernel for the HBM byte counters)")
     ap.add_argument("--blaslt", action="store_true",
                     help="only compare the prefill matmul with dequantize-then-hipBLASLt bf16 GEMM on the same shapes")
+    ap.add_argument("--moe", action="store_true",
+                    help="only time the MoE block rows (T=1 and T=4096) of the configuration table")
     ap.add_argument("--addnorm", action="store_true",
                     help="only time the residual add + RMSNorm matvec against the plain matvec at the north-star shape")
     args = ap.parse_args()
@@ -91,6 +93,10 @@ def main():
         return
     if args.addnorm:
         addnorm_compare(dev, gen)
+        return
+    if args.moe:
+        for r in moe_rows(dev, gen, torch.cuda.Stream()):
+            print(json.dumps(r), flush=True)
         return
     M, N, K, bits, gs = 1, 17408, 5120, 4, 64
 
@@ -330,6 +336,20 @@ def config_table(dev, gen, stream):
         qmm_row("prefill up 4-bit", M, 17408, 5120, 4)
         qmm_row("prefill down 4-bit", M, 5120, 17408, 4)
     qmm_row("prefill up 2-bit", 512, 17408, 5120, 2)
+    rows += moe_rows(dev, gen, stream)
+    return rows
+
+
+def moe_rows(dev, gen, stream):
+    """The MoE block rows (BASELINE config [4]): E=128, k=8, H=2048, I=768, 4-bit gs64; T=1 with rotating
+    router logits (different experts each call) and T=4096."""
+    import torch
+
+    from lisa_amd import ops
+    from lisa_amd.synth import torch_linear, torch_x
+
+    rows = []
+    gs = 64
     # [4] MoE: E=128, k=8, H=2048, I=768 (gate/up/down stacks, 340 MB); T=1 with rotating logits
     # (different experts each call), T=4096
     E, k, H, I = 128, 8, 2048, 768
@@ -343,12 +363,12 @@ def config_table(dev, gen, stream):
         per_expert = 3 * (I * H // 2 + 2 * 2 * I * (H // gs))  # packed W + scales + biases of one expert's 3 matrices
         if T == 1:
             nb = k * per_expert
-            rows.append({"workload": "MoE 4-bit E=128 k=8 (route+sort+gather+gate/up/down+combine)", "T": T,
+            rows.append({"workload": "MoE 4-bit E=128 k=8 (routed block: route, sort, gate|up + SwiGLU, down, combine)", "T": T,
                          "us": round(t * 1e6, 2), "value": round(nb / t / 1e9, 1), "unit": "GB/s",
                          "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nb})
         else:
             fl = 2.0 * T * k * (2 * I * H + H * I)
-            rows.append({"workload": "MoE 4-bit E=128 k=8 (route+sort+gather+gate/up/down+combine)", "T": T,
+            rows.append({"workload": "MoE 4-bit E=128 k=8 (routed block: route, sort, gate|up + SwiGLU, down, combine)", "T": T,
                          "us": round(t * 1e6, 1), "value": round(fl / t / 1e12, 1), "unit": "TFLOP/s",
                          "frac": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4)})
     return rows

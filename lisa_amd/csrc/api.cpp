@@ -559,7 +559,8 @@ int lisaq_gather_rows(void* stream, const void* x, const int32_t* rows, void* ou
 // gate|up tiles of the MoE prefill: every run in 128-row tiles of 128 columns
 static int64_t gu_cap(int64_t R, int64_t I, int E) {
   const int64_t runs = R < E ? R : E;
-  return ((R + kGuBM - 1) / kGuBM + runs) * ((I + kGuBN - 1) / kGuBN);
+  const int BM = qmm_gu_rows(R, E);
+  return ((R + BM - 1) / BM + runs) * ((I + kGuBN - 1) / kGuBN);
 }
 
 // The fused gate|up matmul serves the prefill when the average expert run is
@@ -583,7 +584,7 @@ static int gate_up_swiglu(hipStream_t st, const void* x, const int32_t* xrows, i
   LISAQ_REQUIRE(T > 0 && T * H < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "gate|up: x larger than 2^31 elements");
   LISAQ_REQUIRE(aligned(act, 16), LISAQ_EINVAL_LAYOUT, "gate|up: act must be 16-byte aligned");
   char* gb = (char*)ws;
-  if (int rc = launch_tile_table(st, sorted, offs, R, E, (int)I, /*limit=*/1, 16, kGuBM, kGuBN, nullptr, 0,
+  if (int rc = launch_tile_table(st, sorted, offs, R, E, (int)I, /*limit=*/1, 16, qmm_gu_rows(R, E), kGuBN, nullptr, 0,
                                  (int4*)(gb + 256), (int)cap, (int32_t*)gb))
     return rc;
   QmmParams p{};
@@ -603,7 +604,7 @@ static int gate_up_swiglu(hipStream_t st, const void* x, const int32_t* xrows, i
   p.K = (int)H;
   p.G = (int)(H / gs);
   p.ksplit = 1;
-  return qmm_gu_launch(st, p, bits, gs, (int)cap);
+  return qmm_gu_launch(st, p, bits, gs, (int)cap, qmm_gu_rows(R, E));
 }
 
 extern "C" {

@@ -41,7 +41,9 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
 // Gate|up matmul of the MoE prefill: tile-table launch of `grid` workgroups,
 // y = SwiGLU(x . gate^T, x . up^T) over 128-column output tiles of 128 rows,
 // x rows gathered through p.xrows (qmm_gu.hip).
-int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid);
-constexpr int kGuBM = 128, kGuBN = 128;  // row / output-column tile of qmm_gu_launch
+// rows: the row tile, qmm_gu_rows(R, E) (the tile table's BM).
+int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows);
+constexpr int kGuBN = 128;          // output-column tile of qmm_gu_launch
+int qmm_gu_rows(int64_t R, int E);  // its row tile for R sorted rows over E experts
 
 }  // namespace lisaq

@@ -1,5 +1,6 @@
 // Gate|up matmul of the MoE prefill (the qmm kernel with GU = true): one
-// launch computes both expert projections of each 128-row x 128-column tile,
+// launch computes both expert projections of each 128- or 256-row x 128-column
+// tile,
 // reads the tile's x rows through the sort's row map, and writes SwiGLU of the
 // two -- the reference's gather_qmm(gate), gather_qmm(up), swiglu sequence
 // (crates/lisa-engine/src/models/qwen4/moe.rs:373-413) with the same bits as those
@@ -8,29 +9,43 @@
 
 namespace lisaq {
 
-int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid) {
-  constexpr int MT = kGuBM / 32;
-  static_assert(kGuBN == QmmLds<4, 64, MT, 1, 8>::BN / 2, "gate|up output tile");
-  LISAQ_REQUIRE(p.tiles && p.xrows && p.w2 && p.s2 && p.b2, LISAQ_EINVAL_LAYOUT, "qmm_gu: missing table or stack");
-  LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
+
+// Row tile: 256 rows when the average expert run is at least 192 rows (the
+// dequantized weights then serve twice the rows; measured at E = 128, k = 8,
+// H = 2048, I = 768: T = 4096 313 vs 330 us), else 128 rows (T = 512: 97 vs
+// 131 us, most runs fit one 128-row tile).
+int qmm_gu_rows(int64_t R, int E) {
+  return R >= 192 * (int64_t)E ? 256 : 128;
+}
+
+template <int MT, int NB = 3>
+static int gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid) {
   qmm_fn fn = nullptr;
   auto pick = [&](auto bt) {
     constexpr int B = decltype(bt)::value;
-    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, true>;
-    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, true>;
-    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, true>;
+    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, true, NB>;
+    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, true, NB>;
+    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, true, NB>;
   };
   if (bits == 4) pick(std::integral_constant<int, 4>{});
   if (bits == 2) pick(std::integral_constant<int, 2>{});
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm_gu: bits=%d group_size=%d not supported", bits, gs);
   // the 4-bit ring's size at either code width: the epilogue's gate|up
   // exchange needs that much
-  constexpr int lds = QmmLds<4, 64, MT, 1, 8>::TOTAL;
-  static_assert(lds >= QmmLds<2, 64, MT, 1, 8>::TOTAL, "ring size");
+  constexpr int lds = QmmLds<4, 64, MT, 1, 8, NB>::TOTAL;
+  static_assert(lds >= QmmLds<2, 64, MT, 1, 8, NB>::TOTAL && lds <= 160 * 1024, "ring size");
+  static_assert(kGuBN == QmmLds<4, 64, MT, 1, 8>::BN / 2, "gate|up output tile");
   if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm_gu")) return rc;
   if (grid <= 0) return LISAQ_OK;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(512), lds, stream, p);
   return check_launch("qmm_gu");
+}
+
+int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows) {
+  LISAQ_REQUIRE(p.tiles && p.xrows && p.w2 && p.s2 && p.b2, LISAQ_EINVAL_LAYOUT, "qmm_gu: missing table or stack");
+  LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
+  LISAQ_REQUIRE(rows == 128 || rows == 256, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built", rows);
+  return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
 }  // namespace lisaq

@@ -99,7 +99,6 @@ constexpr int BK = 64;
 // on 16 distinct ones of a 256-byte line, i.e. no bank conflicts whether the
 // LDS serves 8 or 16 lanes of a 128-bit read per clock.
 constexpr int XG = 1024;  // bytes per 8-row group
-constexpr int NBUF = 3;   // LDS ring: step k+2 lands while step k runs
 
 __device__ __forceinline__ int x_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int x_lds_off(int row, int chunk) { return row * 128 + ((chunk ^ x_swz(row)) << 4); }
@@ -143,7 +142,9 @@ __device__ __forceinline__ void block_sync() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BITS, int GS, int MT, int NT, int WN>
+// NB: depth of the LDS rings (x of step k + NB - 1 and W of step k + NB are
+// in flight while step k runs)
+template <int BITS, int GS, int MT, int NT, int WN, int NB = 3>
 struct QmmLds {
   static constexpr int BM = 32 * MT, BN = WN * 32 * NT;
   static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
@@ -151,8 +152,8 @@ struct QmmLds {
   static constexpr int W = BN * RB;                // packed W tile
   static constexpr int S = BN * 4;                 // scales: the aligned bf16 pair holding the step's group(s)
   static constexpr int WSTAGE = W + 2 * S;         // packed W + scales + biases of one step
-  static constexpr int W0 = NBUF * X;              // W ring after the x ring
-  static constexpr int TOTAL = NBUF * (X + WSTAGE);
+  static constexpr int W0 = NB * X;                // W ring after the x ring
+  static constexpr int TOTAL = NB * (X + WSTAGE);
 };
 
 // WN waves side by side along N, each all BM rows x 32*NT columns: four
@@ -168,10 +169,11 @@ struct QmmLds {
 // SwiGLU(bf16 gate, bf16 up) (the arithmetic of moe_dev.h).  x rows are read
 // through p.xrows (no gathered copy of x), and 32-row blocks past the tile's
 // rows skip their matrix instructions (short expert runs).
-template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT, bool GU = false>
+template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT, bool GU = false, int NB = 3>
 __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
-  using L = QmmLds<BITS, GS, MT, NT, WN>;
+  using L = QmmLds<BITS, GS, MT, NT, WN, NB>;
+  static_assert(NB >= 3, "ring depth");
   constexpr int BM = L::BM;
   constexpr int BN = L::BN;
   constexpr int NWV = WN;  // waves per workgroup
@@ -403,9 +405,12 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   issue_x(kc(0), 0, 0, XI);
   issue_w(kc(0), 0);
   issue_w(kc(1), 1);
-  issue_x(kc(1), 1, 0, XI);
-  issue_w(kc(2), 2);
-  wait_vm<VM_X + VM_W>();  // x(0), W(0), W(1) landed (this wave's part)
+  static_for<NB - 2>([&](auto I) {
+    constexpr int i = decltype(I)::value + 1;
+    issue_x(kc(i), i, 0, XI);
+    issue_w(kc(i + 1), i + 1);
+  });
+  wait_vm<(NB - 2) * (VM_X + VM_W)>();  // x(0), W(0), W(1) landed (this wave's part)
   block_sync();
   {
     WLane w0;
@@ -441,10 +446,10 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   static_assert(NCOPY <= 3 * NMF && NPIECE <= SLOTS, "slot plan");
   int xs = 0, ws1 = 1;  // x stage of step k, W stage of step k+1
   auto step = [&](int kt, uint32_t (*bcur)[16], uint32_t (*bnxt)[16], const WLane& wn, WLane& wnn) {
-    const int xs2 = xs == 0 ? 2 : xs - 1;    // (k+2) % 3
-    const int ws3 = ws1 == 0 ? 2 : ws1 - 1;  // (k+3) % 3 = k % 3
-    const int xs1 = xs == 2 ? 0 : xs + 1;    // (k+1) % 3
-    const int ws2 = ws1 == 2 ? 0 : ws1 + 1;  // (k+2) % 3
+    const int xs2 = xs == 0 ? NB - 1 : xs - 1;    // (k+NB-1) % NB: x copy of this step
+    const int ws3 = xs;                           // (k+NB) % NB: W copy of this step
+    const int xs1 = xs == NB - 1 ? 0 : xs + 1;    // (k+1) % NB
+    const int ws2 = ws1 == NB - 1 ? 0 : ws1 + 1;  // (k+2) % NB
     const unsigned char* xb = smem + xs * L::X;
     const unsigned char* xb1 = smem + xs1 * L::X;
     uint32_t lo[NT][G::WPL], hi[NT][G::WPL], c4[NT][G::WPL][4];  // split codes of the words being dequantized
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
       constexpr int nt = i / MT, mt = i % MT;
       if constexpr (i == 0 && j == 3) {
         wait_lgkm0();
-        wait_vm<VM_X + VM_W>();
+        wait_vm<(NB - 2) * (VM_X + VM_W)>();
         block_sync();
       }
       // matrix instruction (issued before the slot's LDS reads, so its operand
@@ -487,8 +492,8 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
       static_for<NCOPY>([&](auto QI) {
         constexpr int q = decltype(QI)::value;
         if constexpr (q * 3 * NMF / NCOPY == sl) {
-          if constexpr (q < XI) issue_x(kc(kt + 2), xs2, q, q + 1);
-          else issue_w_part(kc(kt + 3), ws3, q - XI);
+          if constexpr (q < XI) issue_x(kc(kt + NB - 1), xs2, q, q + 1);
+          else issue_w_part(kc(kt + NB), ws3, q - XI);
         }
       });
       // dequant pieces: piece d at slot d * SLOTS / NPIECE
@@ -536,48 +541,56 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   // accumulators in registers).
   if constexpr (GU) {
     // exchange through LDS (after every copy into the ring has landed and
-    // every wave is past its last read): [2][BM][BN/2 + 8] bf16, gate rows
-    // then up rows, 16 bytes of padding per row against bank conflicts
+    // every wave is past its last read), RB rows at a time:
+    // [2][RB][BN/2 + 8] bf16, gate rows then up rows, 16 bytes of padding per
+    // row against bank conflicts
     constexpr int HN = BN / 2, XS = HN + 8;
+    constexpr int RB = BM <= 128 ? BM : BM % 128 == 0 ? 128 : 64, NPASS = BM / RB, MTP = RB / 32;
     // (launched with the 4-bit ring's LDS size at either code width)
-    static_assert(2 * BM * XS * 2 <= QmmLds<4, GS, MT, NT, WN>::TOTAL, "gate|up exchange fits the ring");
+    static_assert(2 * RB * XS * 2 <= QmmLds<4, GS, MT, NT, WN, NB>::TOTAL && BM % RB == 0,
+                  "gate|up exchange fits the ring");
     wait_vm<0>();
-    wait_lgkm0();
-    block_sync();
     uint16_t* ex = reinterpret_cast<uint16_t*>(smem);
     const int half = wn / (WN / 2), wc = wn % (WN / 2);
+    static_for<NPASS>([&](auto PI) {
+      constexpr int hp = decltype(PI)::value;
+      wait_lgkm0();
+      block_sync();  // (all reads of the ring, or of the previous pass, done)
+      if (hp * RB < M) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+        for (int mt = hp * MTP; mt < (hp + 1) * MTP; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
+          for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x16& a = acc[mt][nt];
-          const int c = (wc * NT + nt) * 32 + 8 * g + 4 * h;
-          *reinterpret_cast<u32x2*>(ex + (half * BM + mt * 32 + col) * XS + c) =
-              u32x2{pk_bf16(a[4 * g], a[4 * g + 1]), pk_bf16(a[4 * g + 2], a[4 * g + 3])};
-        }
-    wait_lgkm0();
-    block_sync();
-    // 8 outputs per thread and pass; N % 8 == 0 (host)
-    constexpr int CH = HN / 8, PASSES = BM * CH / (64 * WN);
-    static_assert(BM * CH % (64 * WN) == 0, "exchange passes");
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      const int c = ps * 64 * WN + (int)threadIdx.x;
-      const int r = c / CH, cc = (c % CH) * 8;
-      if (r >= M || nt0 + cc >= p.N) continue;
-      const u32x4 gv = *reinterpret_cast<const u32x4*>(ex + r * XS + cc);
-      const u32x4 uv = *reinterpret_cast<const u32x4*>(ex + (BM + r) * XS + cc);
-      u32x4 o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t lo = swiglu_bf16(bf2f_lo(gv[j]), bf2f_lo(uv[j]));
-        const uint32_t hi = swiglu_bf16(bf2f_hi(gv[j]), bf2f_hi(uv[j]));
-        o[j] = lo | (hi << 16);
+            for (int g = 0; g < 4; ++g) {
+              const f32x16& a = acc[mt][nt];
+              const int c = (wc * NT + nt) * 32 + 8 * g + 4 * h;
+              *reinterpret_cast<u32x2*>(ex + (half * RB + (mt - hp * MTP) * 32 + col) * XS + c) =
+                  u32x2{pk_bf16(a[4 * g], a[4 * g + 1]), pk_bf16(a[4 * g + 2], a[4 * g + 3])};
+            }
       }
-      *reinterpret_cast<u32x4*>(y + (int64_t)r * p.N + nt0 + cc) = o;
-    }
+      wait_lgkm0();
+      block_sync();
+      // 8 outputs per thread and pass; N % 8 == 0 (host)
+      constexpr int CH = HN / 8, PASSES = RB * CH / (64 * WN);
+      static_assert(RB * CH % (64 * WN) == 0, "exchange passes");
+#pragma unroll
+      for (int ps = 0; ps < PASSES; ++ps) {
+        const int c = ps * 64 * WN + (int)threadIdx.x;
+        const int r = c / CH, cc = (c % CH) * 8;
+        if (hp * RB + r >= M || nt0 + cc >= p.N) continue;
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(ex + r * XS + cc);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(ex + (RB + r) * XS + cc);
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = swiglu_bf16(bf2f_lo(gv[j]), bf2f_lo(uv[j]));
+          const uint32_t hi = swiglu_bf16(bf2f_hi(gv[j]), bf2f_hi(uv[j]));
+          o[j] = lo | (hi << 16);
+        }
+        *reinterpret_cast<u32x4*>(y + (int64_t)(hp * RB + r) * p.N + nt0 + cc) = o;
+      }
+    });
     return;
   }
   const bool vec = (p.N & 3) == 0;
