@@ -15,7 +15,7 @@ namespace lisaq {
 // H = 2048, I = 768: T = 4096 313 vs 330 us), else 128 rows (T = 512: 97 vs
 // 131 us, most runs fit one 128-row tile).
 int qmm_gu_rows(int64_t R, int E) {
-  return R >= 192 * (int64_t)E ? 256 : 128;
+  return tune_int("LISAQ_GU_ROWS", R >= 192 * (int64_t)E ? 256 : 128);
 }
 
 template <int MT, int NB = 3>
