@@ -166,7 +166,9 @@ static size_t up256(size_t v) { return (v + 255) / 256 * 256; }
 // knows one (moe_forward: a token picks an expert at most once, so T);
 // otherwise R.  It only sizes the matvec rows and decides if matmul tiles can
 // occur; the tables still follow the actual runs.
-static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs, int bits, int64_t max_run = 0) {
+// tall: matmul tiles of 256 rows (runs known to average >= 192 rows).
+static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs, int bits, int64_t max_run = 0,
+                                  bool tall = false) {
   GatherLayout L{};
   L.limit = lisaq_qmv_batch_limit(K, N);
   const int64_t runs = R < E ? R : E;
@@ -176,7 +178,7 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   L.qc = qmv_config(L.Mmax, N, K, gs, bits, /*single_pass=*/true);
   L.mc = qmm_config(L.limit, N, K, gs, bits);
   {
-    const int mt = tune_int("LISAQ_GATHER_MT", L.mc.MT);
+    const int mt = tall ? 8 : tune_int("LISAQ_GATHER_MT", L.mc.MT);
     if (mt == 4 || mt == 6 || mt == 8) {
       L.mc.MT = mt;
       L.mc.BM = 32 * mt;
@@ -233,7 +235,7 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
     p.N = (int)N;
     p.K = (int)K;
     p.G = (int)(K / gs);
-    rc = qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
+    rc = L.mc.MT == 8 ? qmm_gather_tall_launch(st, p, bits, gs, L.qmm_cap) : qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
     if (rc) return rc;
   }
   return LISAQ_OK;
@@ -684,6 +686,13 @@ struct MoeLayout {
   size_t idx, wts, sorted, order, rows, inv, offs, hist, xs, g, u, d, gws, total;
 };
 
+// The down projection of the fused-gate|up prefill takes 256-row matmul
+// tiles when runs average >= 192 rows (as the gate|up matmul does).
+static bool moe_down_tall(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
+  return moe_gu_path(T, H, I, E, k, gs, bits) && tune_int("LISAQ_MOE_DOWN_TALL", 1) != 0 &&
+         T * k >= 192 * (int64_t)E;
+}
+
 static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
   MoeLayout L{};
   const int64_t R = T * k;
@@ -708,7 +717,7 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
   // the tables exactly as lisaq_moe_forward lays them out: runs of at most T
   // rows (a token picks an expert once)
   const size_t g1 = gather_layout(R, I, H, E, gs, bits, T).total;
-  const size_t g2 = gather_layout(R, H, I, E, gs, bits, T).total;
+  const size_t g2 = gather_layout(R, H, I, E, gs, bits, T, moe_down_tall(T, H, I, E, k, gs, bits)).total;
   const size_t g3 = 256 + up256((size_t)gu_cap(R, I, E) * 16);
   L.gws = take(g1 > g2 ? (g1 > g3 ? g1 : g3) : (g2 > g3 ? g2 : g3));
   L.total = o;
@@ -772,7 +781,7 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
     if ((rc = gate_up_swiglu(st, x, rows, T, sorted, offs, gw, gsc, gbi, uw, usc, ubi, g, R, I, H, E, gs, bits, gws,
                              gws_bytes)))
       return rc;
-    const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T);
+    const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T, moe_down_tall(T, H, I, E, k, gs, bits));
     LISAQ_REQUIRE(DN.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
     if ((rc = gather_tables(st, DN, sorted, R, H, E, gws, offs))) return rc;
     if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;

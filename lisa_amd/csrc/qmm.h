@@ -45,5 +45,7 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
 int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows);
 constexpr int kGuBN = 128;          // output-column tile of qmm_gu_launch
 int qmm_gu_rows(int64_t R, int E);  // its row tile for R sorted rows over E experts
+// Gather (tile-table) launch with 256-row tiles that skip their empty 32-row blocks.
+int qmm_gather_tall_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid);
 
 }  // namespace lisaq

@@ -48,4 +48,27 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
   return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
+// Gather launches with 256-row tiles (the MoE prefill's down projection when
+// runs average >= 192 rows): the plain kernel with the empty 32-row blocks'
+// matrix instructions skipped (the last tile of a run is mostly empty).
+int qmm_gather_tall_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid) {
+  qmm_fn fn = nullptr;
+  int lds = 0;
+  auto pick = [&](auto bt) {
+    constexpr int B = decltype(bt)::value;
+    lds = QmmLds<B, 64, 8, 1, 8>::TOTAL;
+    if (gs == 32) fn = qmm_kernel<B, 32, 8, 1, 8, false, false, 3, true>;
+    if (gs == 64) fn = qmm_kernel<B, 64, 8, 1, 8, false, false, 3, true>;
+    if (gs == 128) fn = qmm_kernel<B, 128, 8, 1, 8, false, false, 3, true>;
+  };
+  if (bits == 4) pick(std::integral_constant<int, 4>{});
+  if (bits == 2) pick(std::integral_constant<int, 2>{});
+  if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm gather: bits=%d group_size=%d not supported", bits, gs);
+  LISAQ_REQUIRE(p.tiles && p.K % 64 == 0, LISAQ_EINVAL_LAYOUT, "qmm gather: tile table and K %% 64 == 0 required");
+  if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm_gather")) return rc;
+  if (grid <= 0) return LISAQ_OK;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(512), lds, stream, p);
+  return check_launch("qmm_gather");
+}
+
 }  // namespace lisaq

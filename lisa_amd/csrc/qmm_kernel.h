@@ -169,7 +169,10 @@ struct QmmLds {
 // SwiGLU(bf16 gate, bf16 up) (the arithmetic of moe_dev.h).  x rows are read
 // through p.xrows (no gathered copy of x), and 32-row blocks past the tile's
 // rows skip their matrix instructions (short expert runs).
-template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT, bool GU = false, int NB = 3>
+//
+// SKIP (tile-table launches; implied by GU): 32-row blocks past the tile's rows
+// skip their matrix instructions.
+template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT, bool GU = false, int NB = 3, bool SKIP = GU>
 __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
   using L = QmmLds<BITS, GS, MT, NT, WN, NB>;
@@ -245,7 +248,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
 
   // 32-row blocks of this tile that hold rows (the rest are clamped copies of
   // the last row and never stored): their matrix instructions are skipped
-  const int mact = GU ? __builtin_amdgcn_readfirstlane(M - m0 >= BM ? MT : (M - m0 + 31) >> 5) : MT;
+  const int mact = SKIP ? __builtin_amdgcn_readfirstlane(M - m0 >= BM ? MT : (M - m0 + 31) >> 5) : MT;
 
   // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
   // matrix are clamped to the last one, their results are never stored)
@@ -464,7 +467,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
       }
       // matrix instruction (issued before the slot's LDS reads, so its operand
       // wait does not also wait for them)
-      if (!GU || mt == 0 || mt < mact) {
+      if (!SKIP || mt == 0 || mt < mact) {
         const u32x4 aw = (j & 1) ? a1[mt] : a0[mt];
         const u32x4 bw = u32x4{bcur[nt][4 * j], bcur[nt][4 * j + 1], bcur[nt][4 * j + 2], bcur[nt][4 * j + 3]};
         // W as the row operand, x as the column operand: the accumulator is
