@@ -49,7 +49,7 @@ typedef enum {
   LISAQ_EWORKSPACE = 6      /* workspace missing or too small               */
 } lisaq_status;
 
-typedef enum { LISAQ_DTYPE_BF16 = 0, LISAQ_DTYPE_F32 = 1 } lisaq_dtype;
+typedef enum { LISAQ_DTYPE_BF16 = 0, LISAQ_DTYPE_F32 = 1, LISAQ_DTYPE_F16 = 2 } lisaq_dtype;
 
 /* Library version (major*10000 + minor*100 + patch). */
 LISAQ_API int lisaq_version(void);
@@ -74,6 +74,21 @@ LISAQ_API int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t
                            const void* biases, void* y, int64_t M, int64_t N, int64_t K,
                            int transpose, int group_size, int bits, void* workspace,
                            size_t workspace_bytes);
+
+/* quantized_matmul for every compute dtype and code width of the reference
+ * (AO:398-404: x, scales and biases promoted to one dtype T; the caller
+ * passes them, and y, in `dtype`: LISAQ_DTYPE_BF16, _F16 or _F32), bits 2, 4
+ * or 8, group size 32/64/128.  bf16 with 2 or 4 bits is lisaq_quantized_matmul
+ * (same kernels, same workspace).  Otherwise: M < qmv_batch_limit(K, N) takes
+ * the matvec arithmetic (f32, per-group scale*sum(x*q) + bias*sum(x),
+ * QM:767-830, 996-1088), larger M the matmul arithmetic (weights rounded to T
+ * from an f32 fma, f32 accumulation, QM:585-703, 1208-1326); y rounded to T
+ * once.  Those paths use no workspace and are not tuned (one wave per output
+ * row; 64 x 64 f32 tiles). */
+LISAQ_API int lisaq_quantized_matmul_typed(void* stream, const void* x, const uint32_t* w, const void* scales,
+                                           const void* biases, void* y, int64_t M, int64_t N, int64_t K,
+                                           int transpose, int group_size, int bits, int dtype, void* workspace,
+                                           size_t workspace_bytes);
 LISAQ_API size_t lisaq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 
 /* lisaq_quantized_matmul without a workspace argument, for callers that

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblisaq.so")
 
 OK, EINVAL_SHAPE, EINVAL_DTYPE, EINVAL_LAYOUT, EUNSUPPORTED, EHIP, EWORKSPACE = range(7)
-DTYPE_BF16, DTYPE_F32 = 0, 1
+DTYPE_BF16, DTYPE_F32, DTYPE_F16 = 0, 1, 2
 
 _STATUS_NAMES = {
     EINVAL_SHAPE: "EINVAL_SHAPE",
@@ -62,6 +62,7 @@ SIGNATURES = {
     "lisaq_swiglu": (ci, [vp, vp, vp, vp, i64]),
     "lisaq_gather_qmm_swiglu": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ci, ci, ci, vp, sz]),
     "lisaq_gather_qmm_swiglu_workspace": (sz, [i64, i64, ci]),
+    "lisaq_quantized_matmul_typed": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci, ci, vp, sz]),
     "lisaq_moe_decode_supported": (ci, [i64, i64, i64, ci, ci, ci, ci]),
     "lisaq_moe_combine": (ci, [vp, vp, vp, vp, vp, i64, ci, i64]),
     "lisaq_moe_forward": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,

@@ -368,6 +368,37 @@ int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t* w, const
   return run_qmm((hipStream_t)stream, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
 }
 
+int lisaq_quantized_matmul_typed(void* stream, const void* x, const uint32_t* w, const void* s, const void* b,
+                                 void* y, int64_t M, int64_t N, int64_t K, int transpose, int gs, int bits, int dtype,
+                                 void* ws, size_t ws_bytes) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(dtype == LISAQ_DTYPE_BF16 || dtype == LISAQ_DTYPE_F16 || dtype == LISAQ_DTYPE_F32, LISAQ_EINVAL_DTYPE,
+                "quantized_matmul_typed: dtype %d (bf16, f16 or f32)", dtype);
+  if (dtype == LISAQ_DTYPE_BF16 && (bits == 2 || bits == 4))
+    return lisaq_quantized_matmul(stream, x, w, s, b, y, M, N, K, transpose, gs, bits, ws, ws_bytes);
+  LISAQ_REQUIRE(transpose == 1, LISAQ_EINVAL_LAYOUT, "quantized_matmul_typed: only transpose=true supported");
+  LISAQ_REQUIRE(b != nullptr, LISAQ_EINVAL_LAYOUT, "quantized_matmul_typed: affine biases required");
+  LISAQ_REQUIRE(M >= 0 && N >= 0 && K >= 0, LISAQ_EINVAL_SHAPE, "quantized_matmul_typed: negative size");
+  LISAQ_REQUIRE(bits == 2 || bits == 4 || bits == 8, LISAQ_EUNSUPPORTED,
+                "quantized_matmul_typed: bits=%d not supported (2, 4 or 8)", bits);
+  LISAQ_REQUIRE(gs == 32 || gs == 64 || gs == 128, LISAQ_EUNSUPPORTED,
+                "quantized_matmul_typed: group_size=%d not supported (32, 64 or 128)", gs);
+  LISAQ_REQUIRE(K % gs == 0, LISAQ_EINVAL_SHAPE, "quantized_matmul_typed: K=%lld not a multiple of %d", (long long)K,
+                gs);
+  LISAQ_REQUIRE(M < ((int64_t)1 << 31) && N < ((int64_t)1 << 31) && K < ((int64_t)1 << 30), LISAQ_EINVAL_SHAPE,
+                "quantized_matmul_typed: size too large");
+  if (M == 0 || N == 0) return LISAQ_OK;
+  LISAQ_REQUIRE(K > 0, LISAQ_EINVAL_SHAPE, "quantized_matmul_typed: K=0");
+  const size_t el = dtype == LISAQ_DTYPE_F32 ? 4 : 2;
+  LISAQ_REQUIRE(x && w && s && y, LISAQ_EINVAL_LAYOUT, "quantized_matmul_typed: null tensor pointer");
+  LISAQ_REQUIRE(aligned(x, el) && aligned(y, el) && aligned(s, el) && aligned(b, el) && aligned(w, 4),
+                LISAQ_EINVAL_LAYOUT, "quantized_matmul_typed: misaligned tensor");
+  (void)ws;
+  (void)ws_bytes;
+  return launch_typed_mm((hipStream_t)stream, M < lisaq_qmv_batch_limit(K, N), x, w, s, b, y, M, N, K, gs, bits,
+                         dtype);
+}
+
 int lisaq_quantized_matmul_noalloc(void* stream, const void* x, const uint32_t* w, const void* s, const void* b,
                                    void* y, int64_t M, int64_t N, int64_t K, int transpose, int gs, int bits) {
   g_err[0] = 0;

@@ -27,6 +27,10 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, in
                       const uint16_t* usc, const uint16_t* ubi, const uint32_t* dw, const uint16_t* dsc,
                       const uint16_t* dbi, uint16_t* act, uint16_t* out, int64_t T, int64_t H, int64_t I, int E,
                       int k, int gs, int bits);
+// quantized matmul for f16/f32/bf16 and 2/4/8-bit codes (qtyped.hip): the
+// matvec arithmetic when matvec, else the matmul arithmetic
+int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* w, const void* s, const void* b,
+                    void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype);
 constexpr int kTileTableMaxExperts = 16384;
 // gather tile tables from the sorted ids (offs == nullptr) or from the sort's
 // expert offsets [E+1]

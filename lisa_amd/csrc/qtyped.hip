@@ -1,0 +1,204 @@
+// Quantized matmul for the compute dtypes and code widths outside the tuned
+// bf16 2/4-bit kernels: x, scales, biases and y in bf16, f16 or f32 (the
+// reference promotes all four to one dtype, ops/array_ops.rs:398-404) and
+// 2-, 4- or 8-bit codes.
+//
+// Arithmetic contract, per the reference's templates on T:
+//  * matvec (M < qmv_batch_limit; quantized.metal qmv_fast / qmv_wide,
+//    :767-830, 996-1088): f32 throughout -- per 32-code chunk of one group,
+//    y += scale * sum(x * q) + bias * sum(x), weights never rounded; y
+//    rounded to T once;
+//  * matmul (larger M; quantized.metal:1208-1326 with the block loader
+//    :585-703): every weight dequantized to T, w = T(scale * q + bias) from an
+//    f32 fma, then y = x . w^T with f32 accumulation, rounded to T once.
+//
+// These are straightforward kernels (one wave per output row for the
+// matvec, 64 x 64 register-tiled f32 FMA for the matmul): correct for every
+// dtype and width, not tuned -- the bf16 2/4-bit shapes the engine runs take
+// the MFMA kernels instead.
+#include "lisaq_common.h"
+#include "qmv.h"
+
+namespace lisaq {
+
+namespace {
+
+// DT: 0 bf16, 1 f32, 2 f16 (the lisaq_dtype values)
+template <int DT>
+__device__ __forceinline__ float ld(const void* p, int64_t i) {
+  if constexpr (DT == 0) return bf2f(static_cast<const uint16_t*>(p)[i]);
+  else if constexpr (DT == 1) return static_cast<const float*>(p)[i];
+  else return (float)static_cast<const _Float16*>(p)[i];
+}
+// float -> T (round to nearest even) -> float
+template <int DT>
+__device__ __forceinline__ float rnd(float v) {
+  if constexpr (DT == 0) return bf2f(f2bf(v));
+  else if constexpr (DT == 1) return v;
+  else return (float)(_Float16)v;
+}
+template <int DT>
+__device__ __forceinline__ void st(void* p, int64_t i, float v) {
+  if constexpr (DT == 0) static_cast<uint16_t*>(p)[i] = f2bf(v);
+  else if constexpr (DT == 1) static_cast<float*>(p)[i] = v;
+  else static_cast<_Float16*>(p)[i] = (_Float16)v;
+}
+
+// code ci of a packed row (little-endian codes within each u32)
+template <int BITS>
+__device__ __forceinline__ uint32_t code(const uint32_t* row, int ci) {
+  constexpr int PACK = 32 / BITS;
+  return (row[ci / PACK] >> (BITS * (ci % PACK))) & ((1u << BITS) - 1u);
+}
+
+__device__ __forceinline__ float wsum64(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Matvec: a wave per output row n; lane l takes the 32-code chunks l, l+64,
+// ...; the rows of x in groups of MB.
+template <int DT, int BITS, int GS>
+__global__ __launch_bounds__(256) void qmv_typed_kernel(const void* x, const uint32_t* w, const void* s,
+                                                        const void* b, void* y, int M, int N, int K) {
+  constexpr int MB = 4;
+  constexpr int WPC = BITS;  // u32 words per 32-code chunk
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int C = K / 32, G = K / GS;
+  const uint32_t* wrow = w + (int64_t)n * (K / (32 / BITS));
+  for (int m0 = 0; m0 < M; m0 += MB) {
+    float part[MB];
+#pragma unroll
+    for (int r = 0; r < MB; ++r) part[r] = 0.f;
+    for (int c = lane; c < C; c += 64) {
+      uint32_t wv[WPC];
+#pragma unroll
+      for (int i = 0; i < WPC; ++i) wv[i] = wrow[c * WPC + i];
+      const int g = c * 32 / GS;
+      const float sc = ld<DT>(s, (int64_t)n * G + g), bi = ld<DT>(b, (int64_t)n * G + g);
+#pragma unroll
+      for (int r = 0; r < MB; ++r) {
+        const int m = m0 + r;
+        if (m >= M) break;
+        float dot = 0.f, xs = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          const float xv = ld<DT>(x, (int64_t)m * K + c * 32 + j);
+          const float q = (float)((wv[j / (32 / BITS)] >> (BITS * (j % (32 / BITS)))) & ((1u << BITS) - 1u));
+          dot = fmaf(xv, q, dot);
+          xs += xv;
+        }
+        part[r] = fmaf(sc, dot, fmaf(bi, xs, part[r]));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < MB; ++r) {
+      const float t = wsum64(part[r]);
+      if (lane == 0 && m0 + r < M) st<DT>(y, (int64_t)(m0 + r) * N + n, t);
+    }
+  }
+}
+
+// Matmul: 64 x 64 output tile per workgroup, K in steps of 32 through LDS (x
+// and the dequantized, T-rounded weights, both as f32), 4 x 4 outputs per
+// thread.
+template <int DT, int BITS, int GS>
+__global__ __launch_bounds__(256) void qmm_typed_kernel(const void* x, const uint32_t* w, const void* s,
+                                                        const void* b, void* y, int M, int N, int K) {
+  constexpr int BM = 64, BN = 64, BK = 32, PAD = 4;
+  __shared__ float xs[BK][BM + PAD];
+  __shared__ float wt[BK][BN + PAD];
+  const int tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int G = K / GS;
+  const int64_t wrow = K / (32 / BITS);
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += BK) {
+#pragma unroll
+    for (int i = 0; i < BM * BK / 256; ++i) {
+      const int e = tid + 256 * i, r = e / BK, kk = e % BK;
+      xs[kk][r] = m0 + r < M ? ld<DT>(x, (int64_t)(m0 + r) * K + k0 + kk) : 0.f;
+    }
+    {
+      const int r = tid / 4, kq = (tid % 4) * 8;  // 8 codes of row n0 + r
+      const int n = n0 + r;
+      if (n < N) {
+        const uint32_t* row = w + (int64_t)n * wrow;
+        const int g = (k0 + kq) / GS;  // (8 consecutive codes lie in one group: GS >= 32)
+        const float sc = ld<DT>(s, (int64_t)n * G + g), bi = ld<DT>(b, (int64_t)n * G + g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wt[kq + j][r] = rnd<DT>(fmaf(sc, (float)code<BITS>(row, k0 + kq + j), bi));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wt[kq + j][r] = 0.f;
+      }
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int kk = 0; kk < BK; ++kk) {
+      float a[4], c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = xs[kk][ty * 4 + i];
+        c[i] = wt[kk][tx * 4 + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], c[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+      if (m < M && n < N) st<DT>(y, (int64_t)m * N + n, acc[i][j]);
+    }
+}
+
+typedef void (*typed_fn)(const void*, const uint32_t*, const void*, const void*, void*, int, int, int);
+
+template <bool MV, int DT, int BITS>
+typed_fn pick_gs(int gs) {
+  if (gs == 32) return MV ? qmv_typed_kernel<DT, BITS, 32> : qmm_typed_kernel<DT, BITS, 32>;
+  if (gs == 64) return MV ? qmv_typed_kernel<DT, BITS, 64> : qmm_typed_kernel<DT, BITS, 64>;
+  if (gs == 128) return MV ? qmv_typed_kernel<DT, BITS, 128> : qmm_typed_kernel<DT, BITS, 128>;
+  return nullptr;
+}
+
+template <bool MV, int DT>
+typed_fn pick_bits(int bits, int gs) {
+  if (bits == 2) return pick_gs<MV, DT, 2>(gs);
+  if (bits == 4) return pick_gs<MV, DT, 4>(gs);
+  if (bits == 8) return pick_gs<MV, DT, 8>(gs);
+  return nullptr;
+}
+
+template <bool MV>
+typed_fn pick(int dtype, int bits, int gs) {
+  if (dtype == LISAQ_DTYPE_BF16) return pick_bits<MV, 0>(bits, gs);
+  if (dtype == LISAQ_DTYPE_F32) return pick_bits<MV, 1>(bits, gs);
+  if (dtype == LISAQ_DTYPE_F16) return pick_bits<MV, 2>(bits, gs);
+  return nullptr;
+}
+
+}  // namespace
+
+int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* w, const void* s, const void* b,
+                    void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype) {
+  const typed_fn fn = matvec ? pick<true>(dtype, bits, gs) : pick<false>(dtype, bits, gs);
+  if (!fn) return set_error(LISAQ_EUNSUPPORTED, "quantized_matmul_typed: dtype=%d bits=%d gs=%d", dtype, bits, gs);
+  if (matvec)
+    hipLaunchKernelGGL(fn, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, w, s, b, y, (int)M, (int)N, (int)K);
+  else
+    hipLaunchKernelGGL(fn, dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64)), dim3(256), 0, st, x, w, s,
+                       b, y, (int)M, (int)N, (int)K);
+  return check_launch("quantized_matmul_typed");
+}
+
+}  // namespace lisaq

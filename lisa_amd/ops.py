@@ -127,8 +127,38 @@ def quantized_matmul(x, w, scales, biases=None, transpose=True, group_size=64, b
     """``ops::quantized_matmul`` (array_ops.rs:378-493): ``x . dequant(w)^T``.
 
     Dispatch as the reference: M < qmv_batch_limit(K, N) -> matvec kernel
-    (f32 weights), else the MFMA matmul (weights rounded to bf16)."""
-    return _mm("lisaq_quantized_matmul", x, w, scales, biases, transpose, group_size, bits)
+    (f32 weights), else the MFMA matmul (weights rounded to bf16).  x,
+    scales and biases are promoted to one compute dtype first (bf16, f16 or
+    f32, array_ops.rs:398-404); anything but bf16 with 2/4-bit codes goes
+    through ``lisaq_quantized_matmul_typed`` (every dtype, 2/4/8 bits)."""
+    _require(biases is not None, _lib.EINVAL_LAYOUT, "quantized_matmul: affine biases required")
+    dt = torch.promote_types(torch.promote_types(x.dtype, scales.dtype), biases.dtype)
+    if dt == torch.bfloat16 and bits in (2, 4):
+        return _mm("lisaq_quantized_matmul", x, w, scales, biases, transpose, group_size, bits)
+    return _mm_typed(x, w, scales, biases, transpose, group_size, bits, dt)
+
+
+_DTYPE_CODE = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+
+def _mm_typed(x, w, scales, biases, transpose, group_size, bits, dt):
+    _require(transpose, _lib.EINVAL_LAYOUT, "quantized_matmul: only transpose=true supported")
+    _require(dt in _DTYPE_CODE, _lib.EINVAL_DTYPE, f"quantized_matmul: unsupported compute dtype {dt}")
+    for t, name in ((x, "x"), (scales, "scales"), (biases, "biases")):
+        _require(t.is_cuda, _lib.EINVAL_LAYOUT, f"{name} must be a device tensor")
+    x, scales, biases = (t.to(dt).contiguous() for t in (x, scales, biases))
+    w = _u32(w, "w")
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    N = w.shape[0]
+    _require(w.dim() == 2 and w.shape[1] * 32 // bits == K, _lib.EINVAL_SHAPE,
+             f"quantized_matmul: w {tuple(w.shape)} does not match K={K}, bits={bits}")
+    _require(scales.shape == (N, K // group_size) and biases.shape == scales.shape, _lib.EINVAL_SHAPE,
+             f"quantized_matmul: scales/biases {tuple(scales.shape)} != ({N}, {K // group_size})")
+    y = torch.empty(*x.shape[:-1], N, dtype=dt, device=x.device)
+    _lib.call("lisaq_quantized_matmul_typed", _stream(x), x.data_ptr(), w.data_ptr(), scales.data_ptr(),
+              biases.data_ptr(), y.data_ptr(), M, N, K, 1, group_size, bits, _DTYPE_CODE[dt], None, 0)
+    return y
 
 
 def quantized_matmul_serial_rows(x, w, scales, biases=None, transpose=True, group_size=64, bits=4):

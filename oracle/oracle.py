@@ -212,3 +212,48 @@ try:
     _declare()
 except OSError:  # not built yet; build() then lib() will load it
     _lib = None
+
+
+# ---- every compute dtype and code width (lisaq_quantized_matmul_typed) ----
+# x, scales and biases are float arrays holding values of the compute dtype T
+# (bf16, f16 or f32), i.e. after the reference's promotion (AO:398-404).
+
+def _round_to(a, dtype: str) -> np.ndarray:
+    """float32 values rounded to T (nearest even) and back to float32."""
+    a = np.asarray(a, np.float32)
+    if dtype == "bf16":
+        return bf16_to_f32(f32_to_bf16(a))
+    if dtype == "f16":
+        return a.astype(np.float16).astype(np.float32)
+    return a
+
+
+def qmv_typed(x, w, scales, biases, group_size: int, bits: int) -> np.ndarray:
+    """Matvec semantics for any T (QM:767-830, 996-1088): weights never
+    rounded; per group scale*sum(x*q) + bias*sum(x), here in float64; [M, N]
+    float64 (the caller rounds to T)."""
+    x = np.asarray(x, np.float64)
+    K = x.shape[-1]
+    q = unpack(w, K, bits).astype(np.float64)               # [N, K]
+    N, G = q.shape[0], K // group_size
+    xg = x.reshape(x.shape[0], G, group_size)                 # [M, G, gs]
+    qg = q.reshape(N, G, group_size)                          # [N, G, gs]
+    dots = np.einsum("mgk,ngk->mng", xg, qg)                 # [M, N, G]
+    xs = xg.sum(-1)                                           # [M, G]
+    s = np.asarray(scales, np.float64).reshape(N, G)
+    b = np.asarray(biases, np.float64).reshape(N, G)
+    return (dots * s[None] + xs[:, None, :] * b[None]).sum(-1)
+
+
+def qmm_typed(x, w, scales, biases, group_size: int, bits: int, dtype: str) -> np.ndarray:
+    """Matmul semantics for any T (QM:585-703, 1208-1326): each weight is
+    T(fma(scale, q, bias)) (the f32 fma rounded once to f32, then to T), then
+    x . w^T accumulated here in float64; [M, N] float64."""
+    x = np.asarray(x, np.float64)
+    K = x.shape[-1]
+    q = unpack(w, K, bits).astype(np.float64)
+    N, G = q.shape[0], K // group_size
+    s = np.repeat(np.asarray(scales, np.float64).reshape(N, G), group_size, axis=1)
+    b = np.repeat(np.asarray(biases, np.float64).reshape(N, G), group_size, axis=1)
+    wt = _round_to((s * q + b).astype(np.float32), dtype).astype(np.float64)  # s*q exact in f64: one rounding to f32
+    return x @ wt.T

@@ -271,3 +271,41 @@ def test_add_rms_norm_unit_rms(oracle):
     _, normed = oracle.add_rms_norm(x, r, nw, 1e-6)
     ms = (bf16_bits_to_f32(normed).astype(np.float64) ** 2).mean(axis=-1)
     assert np.allclose(ms, 1.0, atol=1e-2)
+
+
+# ---- the typed (any dtype, 2/4/8-bit) restatements ----------------------------
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_typed_restatements_match_the_bf16_oracle(oracle, bits):
+    """On bf16 values the typed numpy restatements agree with the C oracle's
+    qmv and qmm (f32 sums there, float64 here: agreement to f32 precision)."""
+    rng = np.random.default_rng(40 + bits)
+    M, N, K, gs = 3, 17, 256, 64
+    w, s, b = np_linear(rng, N, K, bits, gs)
+    x = np_x(rng, M, K)
+    xf, sf, bf = (bf16_bits_to_f32(a) for a in (x, s, b))
+    mv = oracle.qmv_typed(xf, w, sf, bf, gs, bits)
+    mm = oracle.qmm_typed(xf, w, sf, bf, gs, bits, "bf16")
+    scale = np.abs(mv).max()
+    assert np.abs(mv - oracle.qmv(x, w, s, b, gs, bits)).max() <= 1e-5 * scale
+    assert np.abs(mm - oracle.qmm(x, w, s, b, gs, bits)).max() <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_typed_closed_form_constant_codes(oracle, dtype):
+    """8-bit codes all equal to c and x all ones: every weight of group g is
+    s_g*c + b_g, so y = sum_g gs * (s_g*c + b_g) (matvec, exact weights) and
+    y = sum_g gs * T(s_g*c + b_g) (matmul, weights rounded to T)."""
+    gs, K, N, c = 32, 128, 3, 201
+    word = c | (c << 8) | (c << 16) | (c << 24)
+    w = np.full((N, K // 4), word, np.uint32)
+    rng = np.random.default_rng(7)
+    s = rng.uniform(0.001, 0.01, (N, K // gs)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, (N, K // gs)).astype(np.float32)
+    x = np.ones((2, K), np.float32)
+    exact = (gs * (s.astype(np.float64) * c + b)).sum(1)
+    assert np.allclose(oracle.qmv_typed(x, w, s, b, gs, 8), exact[None], rtol=1e-12)
+    wt = oracle._round_to((s.astype(np.float64) * c + b).astype(np.float32), dtype).astype(np.float64)
+    assert np.allclose(oracle.qmm_typed(x, w, s, b, gs, 8, dtype), (gs * wt).sum(1)[None], rtol=1e-12)
+    if dtype != "f32":  # the rounding to T is really applied
+        assert not np.allclose(wt, s * c + b, rtol=1e-7, atol=0)
