@@ -144,9 +144,9 @@ __device__ __forceinline__ void block_sync() {
 
 // NB: depth of the LDS rings (x of step k + NB - 1 and W of step k + NB are
 // in flight while step k runs)
-template <int BITS, int GS, int MT, int NT, int WN, int NB = 3>
+template <int BITS, int GS, int MT, int NT, int WN, int NB = 3, int WM = 1>
 struct QmmLds {
-  static constexpr int BM = 32 * MT, BN = WN * 32 * NT;
+  static constexpr int BM = 32 * MT * WM, BN = WN * 32 * NT;
   static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
   static constexpr int X = BM / 8 * XG;            // x tile
   static constexpr int W = BN * RB;                // packed W tile
@@ -172,19 +172,24 @@ struct QmmLds {
 //
 // SKIP (tile-table launches; implied by GU): 32-row blocks past the tile's rows
 // skip their matrix instructions.
-template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT, bool GU = false, int NB = 3, bool SKIP = GU>
-__global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
+//
+// WM: waves along M (WN x WM waves, each MT x 32 rows by NT x 32 columns).
+template <int BITS, int GS, int MT, int NT, int WN, bool SPLIT, bool GU = false, int NB = 3, bool SKIP = GU,
+          int WM = 1>
+__global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
-  using L = QmmLds<BITS, GS, MT, NT, WN, NB>;
+  using L = QmmLds<BITS, GS, MT, NT, WN, NB, WM>;
+  static_assert(WM == 1 || (!GU && !SKIP), "waves along M: plain tiles only");
   static_assert(NB >= 3, "ring depth");
   constexpr int BM = L::BM;
   constexpr int BN = L::BN;
-  constexpr int NWV = WN;  // waves per workgroup
+  constexpr int NWV = WN * WM;  // waves per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int wn = wave;  // column group
+  const int wn = WM == 1 ? wave : wave % WN;               // column group
+  const int wrow = WM == 1 ? 0 : (wave / WN) * MT * 32;  // first tile row of the wave's row group
   const int col = lane & 31;
   const int h = lane >> 5;
 
@@ -408,11 +413,16 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   issue_x(kc(0), 0, 0, XI);
   issue_w(kc(0), 0);
   issue_w(kc(1), 1);
-  static_for<NB - 2>([&](auto I) {
-    constexpr int i = decltype(I)::value + 1;
-    issue_x(kc(i), i, 0, XI);
-    issue_w(kc(i + 1), i + 1);
-  });
+  if constexpr (NB == 3) {
+    issue_x(kc(1), 1, 0, XI);
+    issue_w(kc(2), 2);
+  } else {
+    static_for<NB - 2>([&](auto I) {
+      constexpr int i = decltype(I)::value + 1;
+      issue_x(kc(i), i, 0, XI);
+      issue_w(kc(i + 1), i + 1);
+    });
+  }
   wait_vm<(NB - 2) * (VM_X + VM_W)>();  // x(0), W(0), W(1) landed (this wave's part)
   block_sync();
   {
@@ -421,7 +431,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
     dequant_all(w0, bA);
   }
   auto read_a1 = [&](const unsigned char* xb, int j, int mt) -> u32x4 {
-    return *reinterpret_cast<const u32x4*>(xb + x_lds_off(mt * 32 + col, 4 * h + j));
+    return *reinterpret_cast<const u32x4*>(xb + x_lds_off(wrow + mt * 32 + col, 4 * h + j));
   };
   u32x4 a0[MT], a1[MT];
   WLane wA, wB;  // W of the step after the current one (alternating)
@@ -450,7 +460,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   int xs = 0, ws1 = 1;  // x stage of step k, W stage of step k+1
   auto step = [&](int kt, uint32_t (*bcur)[16], uint32_t (*bnxt)[16], const WLane& wn, WLane& wnn) {
     const int xs2 = xs == 0 ? NB - 1 : xs - 1;    // (k+NB-1) % NB: x copy of this step
-    const int ws3 = xs;                           // (k+NB) % NB: W copy of this step
+    const int ws3 = ws1 == 0 ? NB - 1 : ws1 - 1;  // (k+NB) % NB = k % NB: W copy of this step
     const int xs1 = xs == NB - 1 ? 0 : xs + 1;    // (k+1) % NB
     const int ws2 = ws1 == NB - 1 ? 0 : ws1 + 1;  // (k+2) % NB
     const unsigned char* xb = smem + xs * L::X;
@@ -600,7 +610,7 @@ __global__ __launch_bounds__(64 * WN) void qmm_kernel(QmmParams p) {
   auto store = [&](auto put4, auto put1) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int m = m0 + mt * 32 + col;
+      const int m = m0 + wrow + mt * 32 + col;
       if (m >= M) continue;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
@@ -662,6 +672,17 @@ qmm_fn qmm_get_impl(int gs, int MT, int* lds) {
   // split launches exist in two layouts only: per-part partials [S][M][N]
   // with 128-row tiles (small grids) and the hybrid compact layout with
   // 256-row tiles; no other tile height is built with split output
+#ifdef LISAQ_TUNING
+  // 256 x 256 tiles as 2 x 4 waves of 128 rows x 64 columns (halves the x
+  // tile's LDS reads, doubles the dequantization per wave)
+  if (MT == 8 && tune_int("LISAQ_QMM_WM", 1) == 2) {
+    *lds = QmmLds<BITS, 64, 4, 2, 4, 3, 2>::TOTAL;
+    if (gs == 32) return qmm_kernel<BITS, 32, 4, 2, 4, SPLIT, false, 3, false, 2>;
+    if (gs == 64) return qmm_kernel<BITS, 64, 4, 2, 4, SPLIT, false, 3, false, 2>;
+    if (gs == 128) return qmm_kernel<BITS, 128, 4, 2, 4, SPLIT, false, 3, false, 2>;
+    return nullptr;
+  }
+#endif
   if (MT == 8) return one(std::integral_constant<int, 8>{});
   if constexpr (!SPLIT) {
     if (MT == 6) return one(std::integral_constant<int, 6>{});

@@ -304,9 +304,9 @@ def test_rejections_raise(dev):
         ops.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev),
                              transpose=False)
     import torch
-    with pytest.raises(ops.LisaqError, match="dtype"):
-        ops.quantized_matmul(torch.zeros(1, 128, device=dev), to_dev_u32(w, dev), to_dev_bf16(s, dev),
-                             to_dev_bf16(b, dev))
+    with pytest.raises(ops.LisaqError, match="dtype"):  # (f16/f32 are supported; f64 is not)
+        ops.quantized_matmul(torch.zeros(1, 128, device=dev, dtype=torch.float64), to_dev_u32(w, dev),
+                             to_dev_bf16(s, dev), to_dev_bf16(b, dev))
 
 
 @pytest.mark.parametrize("N,K", [(264, 5120), (1000, 9728), (17408, 5120), (16384, 4608)])
