@@ -152,6 +152,8 @@ int qmm_launch(hipStream_t stream, const QmmConfig& c, QmmParams p, int bits, in
     return qmm_launch(stream, c1, p, bits, gs, c1.grid, grid_y, nullptr, 0);
   }
   LISAQ_REQUIRE((int64_t)p.M * p.K < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "qmm: x larger than 2^31 elements");
+  LISAQ_REQUIRE((int64_t)p.N * p.K * bits / 8 < ((int64_t)1 << 32), LISAQ_EINVAL_SHAPE,
+                "qmm: one weight matrix larger than 4 GiB");
   // the two split layouts: per-part [S][M][N] partials with 128-row tiles,
   // hybrid compact parts with 256-row tiles
   if (split && !((c.full_tiles == 0 && c.MT == 4) || (c.full_tiles > 0 && c.MT == 8)))

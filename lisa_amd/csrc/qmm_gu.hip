@@ -43,6 +43,8 @@ static int gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, i
 
 int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows) {
   LISAQ_REQUIRE(p.tiles && p.xrows && p.w2 && p.s2 && p.b2, LISAQ_EINVAL_LAYOUT, "qmm_gu: missing table or stack");
+  LISAQ_REQUIRE((int64_t)p.N * p.K * bits / 8 < ((int64_t)1 << 32), LISAQ_EINVAL_SHAPE,
+                "qmm_gu: one weight matrix larger than 4 GiB");
   LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
   LISAQ_REQUIRE(rows == 128 || rows == 256, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built", rows);
   return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
@@ -65,6 +67,8 @@ int qmm_gather_tall_launch(hipStream_t stream, const QmmParams& p, int bits, int
   if (bits == 2) pick(std::integral_constant<int, 2>{});
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm gather: bits=%d group_size=%d not supported", bits, gs);
   LISAQ_REQUIRE(p.tiles && p.K % 64 == 0, LISAQ_EINVAL_LAYOUT, "qmm gather: tile table and K %% 64 == 0 required");
+  LISAQ_REQUIRE((int64_t)p.N * p.K * bits / 8 < ((int64_t)1 << 32) && (int64_t)p.M * p.K < ((int64_t)1 << 31),
+                LISAQ_EINVAL_SHAPE, "qmm gather: x or one weight matrix too large");
   if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm_gather")) return rc;
   if (grid <= 0) return LISAQ_OK;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(512), lds, stream, p);

@@ -135,6 +135,19 @@ __device__ __forceinline__ void load_lds2(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 2, 0, 0);
 }
 
+// The same through a buffer descriptor: byte address = base + voffset +
+// soffset, with the per-step advance in the scalar soffset (no per-step
+// address arithmetic in the vector registers).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lds_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
+}
+
 // s_waitcnt vmcnt(N) (expcnt, lgkmcnt left alone): the direct-to-LDS loads
 // are not tracked by the compiler's own waits.
 template <int N>
@@ -297,29 +310,38 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
       return (uint32_t)row * (uint32_t)p.K + (xchunk ^ (((wave * XI + i) & 1) << 3));
     }
   };
+  // byte ranges of the copies' descriptors (every offset stays below 2^32:
+  // the host checks x and one weight matrix against it)
+  const __amdgpu_buffer_rsrc_t rx =
+      lds_rsrc(x, (uint32_t)((GU ? (int64_t)p.xrows_max + 1 : (int64_t)M) * p.K * 2));
+  uint32_t xvo[XI];  // byte offset of each x copy (the step's K offset goes in soffset)
+#pragma unroll
+  for (int i = 0; i < XI; ++i) xvo[i] = xoff(i) * 2u;
   // W: BN rows x RB bytes, row-major; 16 bytes per lane: WB bytes per wave in
   // WI instructions (the last lanes idle when a wave's share is under 1 KB)
   constexpr int WB = L::W / NWV;                  // bytes per wave
   constexpr int WI = WB >= 1024 ? WB / 1024 : 1;  // instructions per wave
   constexpr int WLANES = WB >= 1024 ? 64 : WB / 16;
   static_assert(L::W % NWV == 0 && (WB >= 1024 ? WB % 1024 == 0 : WB % 16 == 0), "W tile geometry");
-  const unsigned char* wsrc[WI];
-  const int64_t rowbytes = (int64_t)p.K * BITS / 8;
+  const uint32_t rowbytes = (uint32_t)p.K * BITS / 8;
+  const uint32_t wbytes = (uint32_t)p.N * rowbytes;
+  // (GU: a wave's W share is rows of one stack -- WB bytes are whole rows of
+  // one half of the tile -- so its descriptor is wave-uniform)
+  static_assert(!GU || (L::W / 2) % WB == 0, "gate|up W share");
+  const bool wup = GU && wave * WB >= L::W / 2;
+  const __amdgpu_buffer_rsrc_t rw = lds_rsrc(wup ? (const void*)w2 : (const void*)w, wbytes);
+  uint32_t wvo[WI];
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
     const int off = wave * WB + i * 1024 + lane * 16;  // byte in the W tile
     int rr = off / L::RB;
-    const uint32_t* wb = w;
-    if (GU && rr >= BN / 2) {
-      wb = w2;
-      rr -= BN / 2;
-    }
+    if (GU && rr >= BN / 2) rr -= BN / 2;
     int n = nt0 + rr;
     n = n < p.N ? n : p.N - 1;
     // 4-bit: physical half (off / 16) % 2 of tile row off / 32 holds logical
     // half ^ w_swz(row)
     const int lb = BITS == 4 ? (off % L::RB) ^ (w_swz(off / L::RB) << 4) : off % L::RB;
-    wsrc[i] = reinterpret_cast<const unsigned char*>(wb) + n * rowbytes + lb;
+    wvo[i] = (uint32_t)n * rowbytes + (uint32_t)lb;
   }
   // scales / biases: per row the 4-byte-aligned bf16 pair holding the step's
   // group(s); 64 rows per instruction (BN/64 instructions per array, spread
@@ -331,37 +353,43 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   // copies i0 <= i < i1 of the x tile (i0, i1 compile-time after inlining)
   auto issue_x = [&](int k, int stage, int i0, int i1) {
     unsigned char* st = smem + stage * L::X;
-    const int k0 = k * BK;
+    const uint32_t k0 = (uint32_t)k * BK;
 #pragma unroll
     for (int i = 0; i < XI; ++i)
-      if (i >= i0 && i < i1) load_lds16(x + xoff(i) + k0, st + (wave * XI + i) * XG);
+      if (i >= i0 && i < i1) buf_lds16(rx, xvo[i], k0 * 2u, st + (wave * XI + i) * XG);
   };
+  // scale/bias copies: the wave's descriptor (wave-uniform: which array, which
+  // stack) and each lane's row offset nb * G
+  const uint32_t sbytes = (uint32_t)p.N * p.G * 2;
+  __amdgpu_buffer_rsrc_t rsb[SBI];
+  uint32_t sbrow[SBI];
+#pragma unroll
+  for (int q = 0; q < SBI; ++q) {
+    const int idx = wave + NWV * q;  // 0 .. 2*SI-1: s row blocks, then b row blocks
+    const bool is_b = idx >= SI;
+    const int blk = is_b ? idx - SI : idx;
+    const bool up = GU && blk >= SI / 2;
+    const uint16_t* base = is_b ? (up ? bi2 : bi) : (up ? sc2 : sc);
+    rsb[q] = lds_rsrc(base, sbytes);
+    const int nb = nt0 + (up ? blk - SI / 2 : blk) * 64 + lane;
+    sbrow[q] = (uint32_t)(nb < p.N ? nb : p.N - 1) * (uint32_t)p.G;
+  }
   // copy q of the W stage of step k: q < WI packed W, else scale/bias copy q - WI
   auto issue_w_part = [&](int k, int stage, int q) {
     unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
     const int k0 = k * BK;
     if (q < WI) {
-      if (WLANES == 64 || lane < WLANES) load_lds16(wsrc[q] + (int64_t)k0 * BITS / 8, st + wave * WB + q * 1024);
+      if (WLANES == 64 || lane < WLANES) buf_lds16(rw, wvo[q], (uint32_t)k0 * BITS / 8, st + wave * WB + q * 1024);
       return;
     }
     const int g = k0 / GS;
     const int idx = wave + NWV * (q - WI);  // 0 .. 2*SI-1: s row blocks, then b row blocks
     const bool is_b = idx >= SI;
     const int blk = is_b ? idx - SI : idx;
-    // (lanes of this instruction load tile rows blk*64 + lane; GU: the second
-    // half of the blocks from the up stack)
-    const bool up = GU && blk >= SI / 2;
-    const int nb = nt0 + (up ? blk - SI / 2 : blk) * 64 + lane;
-    const int64_t roff = (int64_t)(nb < p.N ? nb : p.N - 1) * p.G + g;
-    // (the stack by wave-uniform arithmetic: a select over four pointers
-    // becomes a lookup table in scratch memory)
-    uintptr_t base = reinterpret_cast<uintptr_t>(is_b ? bi : sc);
-    if constexpr (GU)
-      base += up ? (is_b ? reinterpret_cast<uintptr_t>(bi2) - reinterpret_cast<uintptr_t>(bi)
-                         : reinterpret_cast<uintptr_t>(sc2) - reinterpret_cast<uintptr_t>(sc))
-                 : 0;
-    const uint16_t* src = reinterpret_cast<const uint16_t*>(base) + (roff & ~(int64_t)1);  // (G is even: 4-byte aligned)
-    load_lds4(src, st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
+    // (lanes of this instruction load tile rows blk*64 + lane: the aligned
+    // bf16 pair holding element nb * G + g)
+    buf_lds4(rsb[q - WI], ((sbrow[q - WI] + (uint32_t)g) & ~1u) * 2u, 0u,
+               st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
   };
   auto issue_w = [&](int k, int stage) {
 #pragma unroll
