@@ -673,6 +673,55 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
         }
     }
   };
+  if constexpr (WM == 1) {
+    if (whole && !p.tiles && (p.N & 7) == 0) {
+      // (plain launches: a gather tile is often a few rows, which the direct
+      // stores below serve for less)
+      // whole tile through LDS, RB rows at a time ([RB][BN + 8] bf16, 16 bytes
+      // of padding per row), then 16-byte stores along the output rows (a
+      // row of the tile is BN * 2 contiguous bytes of y), after every copy into
+      // the ring has landed (the copies past the last step re-read it) and
+      // every wave is past its last ring read.
+      constexpr int XSn = BN + 8;
+      constexpr int RB = BM * XSn * 2 <= L::TOTAL ? BM : (BM % 128 == 0 && 128 * XSn * 2 <= L::TOTAL) ? 128 : 96;
+      constexpr int NPASS = BM / RB, MTP = RB / 32;
+      static_assert(RB * XSn * 2 <= L::TOTAL && BM % RB == 0, "output tile exchange fits the ring");
+      constexpr int CH = BN / 8, PASSES = RB * CH / (64 * NWV);
+      static_assert(RB * CH % (64 * NWV) == 0, "output passes");
+      wait_vm<0>();
+      uint16_t* ex = reinterpret_cast<uint16_t*>(smem);
+      static_for<NPASS>([&](auto PI) {
+        constexpr int hp = decltype(PI)::value;
+        wait_lgkm0();
+        block_sync();
+        if (hp * RB < M - m0) {
+#pragma unroll
+          for (int mt = hp * MTP; mt < (hp + 1) * MTP; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                const f32x16& a = acc[mt][nt];
+                const int c = (wn * NT + nt) * 32 + 8 * g + 4 * h;
+                *reinterpret_cast<u32x2*>(ex + ((mt - hp * MTP) * 32 + col) * XSn + c) =
+                    u32x2{pk_bf16(a[4 * g], a[4 * g + 1]), pk_bf16(a[4 * g + 2], a[4 * g + 3])};
+              }
+        }
+        wait_lgkm0();
+        block_sync();
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+          const int c = ps * 64 * NWV + (int)threadIdx.x;
+          const int r = c / CH, cc = (c % CH) * 8;
+          const int m = m0 + hp * RB + r;
+          if (m >= M || nt0 + cc >= p.N) continue;
+          *reinterpret_cast<u32x4*>(y + (int64_t)m * p.N + nt0 + cc) =
+              *reinterpret_cast<const u32x4*>(ex + r * XSn + cc);
+        }
+      });
+      return;
+    }
+  }
   if (whole) {
     store([&](int m, int n, float v0, float v1, float v2, float v3) {
             *reinterpret_cast<u32x2*>(y + (int64_t)m * p.N + n) = u32x2{pk_bf16(v0, v1), pk_bf16(v2, v3)};
