@@ -217,6 +217,9 @@ def _time_graph(stream, fn, n_sets, steps, warm_s=CLOCK_WARM_S):
     (steady clock; the first replays of a new graph over new buffers run slow)."""
     import torch
 
+    # inputs were made on the current stream; the calls below share library
+    # workspaces with any eager call still queued there
+    stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         for i in range(n_sets):
             fn(i)
