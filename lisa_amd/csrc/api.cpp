@@ -155,6 +155,7 @@ static int run_qmm(hipStream_t st, const void* x, const uint32_t* w, const void*
 // Gather workspace layout: [counts 256 B][qmv table][qmm table], 256-B aligned.
 struct GatherLayout {
   int limit, Mmax, qmv_cap, qmm_cap;
+  int qmv_grid;  // matvec launch grid (qmv_cap, or a short grid walking the table)
   size_t qmv_off, qmm_off, total;
   QmvConfig qc;
   QmmConfig mc;
@@ -186,6 +187,11 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   }
   L.qmv_cap = (int)(runs * ((N + L.qc.tile_rows - 1) / L.qc.tile_rows));
   L.qmm_cap = (mr >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
+  // Runs averaging >= 4x the matvec limit leave few (usually no) runs to the
+  // matvec: a block per table entry would spend ~10 us dispatching blocks that
+  // find no tile, so a short grid walks the table instead.
+  L.qmv_grid = L.qmv_cap;
+  if (L.qc.kind == 2 && R >= 4 * (int64_t)L.limit * E && L.qmv_cap > kQmvtWalkGrid) L.qmv_grid = kQmvtWalkGrid;
   L.qmv_off = 256;
   L.qmm_off = L.qmv_off + up256((size_t)L.qmv_cap * 16);
   L.total = L.qmm_off + up256((size_t)L.qmm_cap * 16);
@@ -220,7 +226,9 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
     p.K = (int)K;
     p.G = (int)(K / gs);
     p.part_rows = (int)R;
-    rc = qmv_launch(st, L.qc, p, bits, gs, L.qmv_cap);
+    p.tile_cap = L.qmv_cap;
+    p.tile_stride = L.qmv_grid < L.qmv_cap ? L.qmv_grid : 0;
+    rc = qmv_launch(st, L.qc, p, bits, gs, L.qmv_grid);
     if (rc) return rc;
   }
   if (L.qmm_cap > 0) {

@@ -137,15 +137,19 @@ __device__ __forceinline__ void load_lds2(const void* g, void* lds) {
 
 // The same through a buffer descriptor: byte address = base + voffset +
 // soffset, with the per-step advance in the scalar soffset (no per-step
-// address arithmetic in the vector registers).
+// address arithmetic in the vector registers).  soffset is wave-uniform at
+// every call; readfirstlane states it, where the compiler would otherwise keep
+// it in a vector register and wrap each copy in a loop over its distinct values.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t lds_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 __device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 __device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff,
+                                           __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 
 // s_waitcnt vmcnt(N) (expcnt, lgkmcnt left alone): the direct-to-LDS loads

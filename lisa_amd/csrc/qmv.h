@@ -4,6 +4,9 @@
 
 namespace lisaq {
 
+// grid of a tile-table launch of the streaming matvec that walks its table
+constexpr int kQmvtWalkGrid = 1024;
+
 struct QmvParams {
   const uint16_t* x;     // [rows, K] bf16
   const uint32_t* w;     // [(E,) N, K/pack]
@@ -12,6 +15,8 @@ struct QmvParams {
   uint16_t* y;           // [rows, N] bf16
   float* partial;        // [S, part_rows, N] f32 (split-K only)
   const int4* tiles;     // gather: {expert, row start, rows, n tile} per block, or null
+  int tile_cap;          // gather: table entries
+  int tile_stride;       // gather: > 0: each block walks the table with this stride (the grid)
   int M;                 // rows (max rows per tile for gather)
   int N, K, G;           // G = K / group_size
   int part_rows;         // rows of the partial buffer

@@ -130,7 +130,7 @@ __host__ __device__ inline QmvtLds qmvt_layout(int SG, int GS, int M, int MQ, in
 // by side (tiles per block, 1 for tile-table launches), which share the
 // staged x: fewer x stagings per row at several rows of x.
 template <int BITS, int GS, int MQ, int MR, int SB, int NW, int D>
-__global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
+__device__ __forceinline__ void qmvt_tile(const QmvParams& p, int bx) {
   constexpr int PACK = 32 / BITS;
   constexpr int GB = GS * BITS / 8;      // bytes of one group in a row
   constexpr int GPS = SB / GB;           // groups per W slab
@@ -157,10 +157,10 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
   const uint16_t* bi = p.b;
   const uint16_t* x = p.x;
   uint16_t* y = p.y;
-  int n0 = (blockIdx.x * tpb + wt) * 16;
+  int n0 = (bx * tpb + wt) * 16;
   int M = p.M;
   if (p.tiles) {
-    const int4 t = p.tiles[blockIdx.x];
+    const int4 t = p.tiles[bx];
     if (t.x < 0) return;
     const int64_t e = t.x;
     w += e * (int64_t)p.N * (p.K / PACK);
@@ -443,6 +443,24 @@ __global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
     }
 }
 
+// One tile per block.
+template <int BITS, int GS, int MQ, int MR, int SB, int NW, int D>
+__global__ __launch_bounds__(512) void qmvt_kernel(QmvParams p) {
+  qmvt_tile<BITS, GS, MQ, MR, SB, NW, D>(p, blockIdx.x);
+}
+
+// Tile-table launch over a short grid (tile_stride blocks): block b takes the
+// tiles b, b + tile_stride, ... up to the first empty entry (the table is
+// compacted) -- for tables where few of the tile_cap entries are expected to
+// hold a tile.  (A separate kernel: the loop raises the register count.)
+template <int BITS, int GS, int MQ, int MR, int SB, int NW, int D>
+__global__ __launch_bounds__(512) void qmvt_walk_kernel(QmvParams p) {
+  for (int i = blockIdx.x; i < p.tile_cap && p.tiles[i].x >= 0; i += p.tile_stride) {
+    if (i != (int)blockIdx.x) __syncthreads();  // (the tile before has read its LDS)
+    qmvt_tile<BITS, GS, MQ, MR, SB, NW, D>(p, i);
+  }
+}
+
 // y = bf16(sum over the S parts of the f32 partials [S][M][N]), parts added in order.
 __global__ __launch_bounds__(256) void qmvt_split_reduce_kernel(const float* __restrict__ part,
                                                                 uint16_t* __restrict__ y, int64_t MN, int S) {
@@ -534,35 +552,38 @@ int qmvt_lds_bytes(const QmvConfig& c, int gs, int M, int bits) {
 typedef void (*qmvt_fn)(QmvParams);
 
 template <int BITS, int GS, int MQ, int MR, int SB>
-static qmvt_fn pick_nw(int NW) {
+static qmvt_fn pick_nw(int NW, bool walk) {
   constexpr int D = (MQ == 1) ? (SB == 256 ? 2 : 3) : 2;
-  if (NW == 4) return qmvt_kernel<BITS, GS, MQ, MR, SB, 4, D>;
-  if (NW == 8) return qmvt_kernel<BITS, GS, MQ, MR, SB, 8, D>;
+  if (NW == 4) return walk ? qmvt_walk_kernel<BITS, GS, MQ, MR, SB, 4, D> : qmvt_kernel<BITS, GS, MQ, MR, SB, 4, D>;
+  if (NW == 8) return walk ? qmvt_walk_kernel<BITS, GS, MQ, MR, SB, 8, D> : qmvt_kernel<BITS, GS, MQ, MR, SB, 8, D>;
   return nullptr;
 }
 
 template <int BITS, int GS, int SB>
-static qmvt_fn pick_m(int MQ, int MR, int NW) {
-  if (MQ == 2) return pick_nw<BITS, GS, 2, 4, SB>(NW);
-  if (MR == 1) return pick_nw<BITS, GS, 1, 1, SB>(NW);
-  if (MR == 2) return pick_nw<BITS, GS, 1, 2, SB>(NW);
-  return pick_nw<BITS, GS, 1, 4, SB>(NW);
+static qmvt_fn pick_m(int MQ, int MR, int NW, bool walk) {
+  if (MQ == 2) return pick_nw<BITS, GS, 2, 4, SB>(NW, walk);
+  if (MR == 1) return pick_nw<BITS, GS, 1, 1, SB>(NW, walk);
+  if (MR == 2) return pick_nw<BITS, GS, 1, 2, SB>(NW, walk);
+  return pick_nw<BITS, GS, 1, 4, SB>(NW, walk);
 }
 
 template <int BITS, int GS>
-static qmvt_fn pick_t(int MQ, int MR, int SB, int NW) {
-  if (SB == 256) return pick_m<BITS, GS, 256>(MQ, MR, NW);
-  if (SB == 128) return pick_m<BITS, GS, 128>(MQ, MR, NW);
+static qmvt_fn pick_t(int MQ, int MR, int SB, int NW, bool walk) {
+  if (SB == 256) return pick_m<BITS, GS, 256>(MQ, MR, NW, walk);
+  if (SB == 128) return pick_m<BITS, GS, 128>(MQ, MR, NW, walk);
   return nullptr;
 }
 
 int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
+  const bool walk = p.tiles && p.tile_stride > 0;
+  if (walk && (grid_x != p.tile_stride || p.tile_cap <= 0))
+    return set_error(LISAQ_EINVAL_LAYOUT, "qmvt: walking grid %d != stride %d", grid_x, p.tile_stride);
   qmvt_fn fn = nullptr;
-  if (bits == 4 && gs == 64) fn = pick_t<4, 64>(c.MQ, c.MR, c.U, c.NW);
-  else if (bits == 4 && gs == 32) fn = pick_t<4, 32>(c.MQ, c.MR, c.U, c.NW);
-  else if (bits == 4 && gs == 128) fn = pick_t<4, 128>(c.MQ, c.MR, c.U, c.NW);
-  else if (bits == 2 && gs == 64) fn = pick_t<2, 64>(c.MQ, c.MR, c.U, c.NW);
-  else if (bits == 2 && gs == 128) fn = pick_t<2, 128>(c.MQ, c.MR, c.U, c.NW);
+  if (bits == 4 && gs == 64) fn = pick_t<4, 64>(c.MQ, c.MR, c.U, c.NW, walk);
+  else if (bits == 4 && gs == 32) fn = pick_t<4, 32>(c.MQ, c.MR, c.U, c.NW, walk);
+  else if (bits == 4 && gs == 128) fn = pick_t<4, 128>(c.MQ, c.MR, c.U, c.NW, walk);
+  else if (bits == 2 && gs == 64) fn = pick_t<2, 64>(c.MQ, c.MR, c.U, c.NW, walk);
+  else if (bits == 2 && gs == 128) fn = pick_t<2, 128>(c.MQ, c.MR, c.U, c.NW, walk);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmvt: bits=%d gs=%d MQ=%d SB=%d NW=%d", bits, gs, c.MQ, c.U, c.NW);
   p.S = p.tiles ? 1 : c.S;
   p.S_inner = c.S_inner;

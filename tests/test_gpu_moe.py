@@ -119,6 +119,27 @@ def test_gather_qmm_short_runs(dev, oracle, monkeypatch, kernel, R, E, N, K):
     assert_close_bf16(from_dev_bf16(y), ref, what=f"gather[{kernel}] R={R} E={E} N={N} K={K}")
 
 
+@pytest.mark.parametrize("kernel", [None, "t"])
+def test_gather_qmm_walking_grid(dev, oracle, monkeypatch, kernel):
+    """Long runs with a dozen short ones among them: R >= 4 x the matvec limit x E, so the matvec's
+    tile-table launch is a short grid whose blocks walk the table (1,536 matvec tiles over 1,024
+    blocks: some blocks take two)."""
+    if kernel:
+        monkeypatch.setenv("LISAQ_QMV_KERNEL", kernel)
+    E, N, K = 16, 2048, 512
+    limit = ops.qmv_batch_limit(K, N)
+    rng = np.random.default_rng(2024)
+    W, S, B = _expert_stack(rng, E, N, K)
+    lens = [int(v) for v in rng.integers(1, limit, 12)] + [600, 700, 650, 555]
+    assert sum(lens) >= 4 * limit * E
+    ids = np.concatenate([np.full(n, e, np.int32) for e, n in enumerate(lens)])
+    x = np_x(rng, ids.size, K)
+    y = ops.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(W, dev), to_dev_bf16(S, dev), to_dev_bf16(B, dev),
+                       rhs_indices=to_dev(ids, dev), group_size=64, bits=4)
+    ref = _gather_ref(oracle, x, W, S, B, ids, limit)
+    assert_close_bf16(from_dev_bf16(y), ref, what=f"gather walking grid [{kernel}]")
+
+
 @pytest.mark.parametrize("T", [1, 4, 64])
 def test_moe_forward_parity(dev, oracle, T):
     """Whole routed SwitchGLU vs the oracle chain, with the reference shapes
