@@ -199,12 +199,15 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
 }
 
 // Tile tables of a gather (runs of the sorted ids) into the workspace.
+static TileTableJob gather_job(const GatherLayout& L, int64_t N, void* ws) {
+  char* base = (char*)ws;
+  return TileTableJob{(int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN, (int4*)(base + L.qmv_off), L.qmv_cap,
+                      (int4*)(base + L.qmm_off), L.qmm_cap, (int32_t*)base};
+}
 static int gather_tables(hipStream_t st, const GatherLayout& L, const int32_t* rhs, int64_t R, int64_t N, int E,
                          void* ws, const int32_t* offs = nullptr) {
-  char* base = (char*)ws;
-  return launch_tile_table(st, rhs, offs, R, E, (int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN,
-                           (int4*)(base + L.qmv_off), L.qmv_cap, (int4*)(base + L.qmm_off), L.qmm_cap,
-                           (int32_t*)base);
+  const TileTableJob job = gather_job(L, N, ws);
+  return launch_tile_table(st, rhs, offs, R, E, &job, 1);
 }
 
 // The matvec and matmul launches over built tables (several weight stacks of
@@ -612,12 +615,20 @@ static bool moe_gu_path(int64_t T, int64_t H, int64_t I, int E, int k, int gs, i
          (bits == 4 || bits == 2) && (gs == 32 || gs == 64 || gs == 128) && T * H < ((int64_t)1 << 31);
 }
 
+// The gate|up matmul's tile table: {cap entries at ws + 256, counts at ws}
+static TileTableJob gu_job(int64_t R, int64_t I, int E, void* ws) {
+  char* gb = (char*)ws;
+  return TileTableJob{(int)I, /*limit=*/1, 16, qmm_gu_rows(R, E), kGuBN, nullptr, 0, (int4*)(gb + 256),
+                      (int)gu_cap(R, I, E), (int32_t*)gb};
+}
+
 // Gate|up + SwiGLU over sorted rows: tile table (from the expert offsets
-// when the caller has them, else from the sorted ids), then one matmul launch.
+// when the caller has them, else from the sorted ids; already built when
+// table_ready), then one matmul launch.
 static int gate_up_swiglu(hipStream_t st, const void* x, const int32_t* xrows, int64_t T, const int32_t* sorted,
                           const int32_t* offs, const uint32_t* gw, const void* gsc, const void* gbi,
                           const uint32_t* uw, const void* usc, const void* ubi, void* act, int64_t R, int64_t I,
-                          int64_t H, int E, int gs, int bits, void* ws, size_t ws_bytes) {
+                          int64_t H, int E, int gs, int bits, void* ws, size_t ws_bytes, bool table_ready = false) {
   const int64_t cap = gu_cap(R, I, E);
   LISAQ_REQUIRE(ws != nullptr && 256 + (size_t)cap * 16 <= ws_bytes && aligned(ws, 256), LISAQ_EWORKSPACE,
                 "gate|up: 256-byte aligned workspace of %zu bytes required (got %zu)", 256 + (size_t)cap * 16,
@@ -625,9 +636,10 @@ static int gate_up_swiglu(hipStream_t st, const void* x, const int32_t* xrows, i
   LISAQ_REQUIRE(T > 0 && T * H < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "gate|up: x larger than 2^31 elements");
   LISAQ_REQUIRE(aligned(act, 16), LISAQ_EINVAL_LAYOUT, "gate|up: act must be 16-byte aligned");
   char* gb = (char*)ws;
-  if (int rc = launch_tile_table(st, sorted, offs, R, E, (int)I, /*limit=*/1, 16, qmm_gu_rows(R, E), kGuBN, nullptr, 0,
-                                 (int4*)(gb + 256), (int)cap, (int32_t*)gb))
-    return rc;
+  if (!table_ready) {
+    const TileTableJob job = gu_job(R, I, E, ws);
+    if (int rc = launch_tile_table(st, sorted, offs, R, E, &job, 1)) return rc;
+  }
   QmmParams p{};
   p.x = (const uint16_t*)x;
   p.w = gw;
@@ -758,7 +770,9 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
   const size_t g1 = gather_layout(R, I, H, E, gs, bits, T).total;
   const size_t g2 = gather_layout(R, H, I, E, gs, bits, T, moe_down_tall(T, H, I, E, k, gs, bits)).total;
   const size_t g3 = 256 + up256((size_t)gu_cap(R, I, E) * 16);
-  L.gws = take(g1 > g2 ? (g1 > g3 ? g1 : g3) : (g2 > g3 ? g2 : g3));
+  // (the gate|up path keeps the down tables and the gate|up table side by
+  // side: both are built by one launch)
+  L.gws = take(g1 > up256(g2) + g3 ? g1 : up256(g2) + g3);
   L.total = o;
   return L;
 }
@@ -817,12 +831,16 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
     if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, d, R, H, I, 1, gs, bits))) return rc;
-    if ((rc = gate_up_swiglu(st, x, rows, T, sorted, offs, gw, gsc, gbi, uw, usc, ubi, g, R, I, H, E, gs, bits, gws,
-                             gws_bytes)))
-      return rc;
+    // tables: the down gather's at gws, the gate|up matmul's after them, both
+    // from the expert offsets in one launch
     const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T, moe_down_tall(T, H, I, E, k, gs, bits));
-    LISAQ_REQUIRE(DN.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
-    if ((rc = gather_tables(st, DN, sorted, R, H, E, gws, offs))) return rc;
+    const size_t gu_at = up256(DN.total);
+    LISAQ_REQUIRE(gu_at <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
+    const TileTableJob jobs[2] = {gather_job(DN, H, gws), gu_job(R, I, E, (char*)gws + gu_at)};
+    if ((rc = launch_tile_table(st, sorted, offs, R, E, jobs, 2))) return rc;
+    if ((rc = gate_up_swiglu(st, x, rows, T, sorted, offs, gw, gsc, gbi, uw, usc, ubi, g, R, I, H, E, gs, bits,
+                             (char*)gws + gu_at, gws_bytes - gu_at, /*table_ready=*/true)))
+      return rc;
     if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;
     return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
   }

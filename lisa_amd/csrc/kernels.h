@@ -32,11 +32,21 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, in
 int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* w, const void* s, const void* b,
                     void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype);
 constexpr int kTileTableMaxExperts = 16384;
-// gather tile tables from the sorted ids (offs == nullptr) or from the sort's
-// expert offsets [E+1]
-int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E, int N, int limit,
-                      int VR, int BM, int BN, int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap,
-                      int32_t* counts);
+// One set of gather tile tables: N output rows per expert, runs shorter
+// than `limit` as matvec tiles of VR rows, the others as BM x BN matmul tiles;
+// counts[0..2]: matvec tiles, matmul tiles, overflow/bad-ids flag.
+struct TileTableJob {
+  int N, limit, VR, BM, BN;
+  int4* qmv_tab;
+  int qmv_cap;
+  int4* qmm_tab;
+  int qmm_cap;
+  int32_t* counts;
+};
+// gather tile tables (one workgroup per job, 1 or 2 jobs) from the sorted ids
+// (offs == nullptr) or from the sort's expert offsets [E+1]
+int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E,
+                      const TileTableJob* jobs, int njobs);
 // stable counting sort over many workgroups; hist: sort_hist_ints(R, E) ints of workspace
 int sort_hist_ints(int64_t R, int E);
 int launch_sort_parallel(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,

@@ -142,7 +142,7 @@ int launch_sort(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k,
 // invalid ids); pass 3 places each block's ids in input order, exactly as the
 // one-workgroup sort places a chunk.  All loads of a block are issued
 // together.
-constexpr int kSortChunk = 2048;
+constexpr int kSortChunk = 512;
 constexpr int kSortPer = kSortChunk / 256;  // ids per thread
 
 __global__ __launch_bounds__(256) void sort_count_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
@@ -172,26 +172,22 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ h
   __shared__ int wsum[16], s_bad;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // per expert: exclusive prefix over the blocks (16 loads in flight at a time)
-  int total = 0;
-  if (tid == 0) {  // invalid ids (row E)
-    int nb = 0;
-    for (int b = 0; b < B; ++b) nb += hist[(int64_t)E * B + b];
-    s_bad = nb;
-  }
-  if (tid < E) {
-    int32_t* row = hist + (int64_t)tid * B;
+  auto row_sum = [&](const int32_t* row) {
+    int t = 0;
     for (int b0 = 0; b0 < B; b0 += 16) {
       int c[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) c[u] = b0 + u < B ? row[b0 + u] : 0;
 #pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (b0 + u < B) {
-          row[b0 + u] = total;
-          total += c[u];
-        }
+      for (int u = 0; u < 16; ++u) t += c[u];
     }
-  }
+    return t;
+  };
+  if (tid == 0) s_bad = row_sum(hist + (int64_t)E * B);  // invalid ids (row E)
+  // (pass 1 reads the expert's row for its total; pass 2, after the scan over
+  // the experts, reads it again and writes the final positions: no
+  // read-after-write chains through memory)
+  const int total = tid < E ? row_sum(hist + (int64_t)tid * B) : 0;
   // exclusive scan of the expert totals (E <= 1024: one per thread)
   const int mine = tid < E ? total : 0;
   int inc = mine;
@@ -207,7 +203,18 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ h
   const int off = base + inc - mine;
   if (tid < E) {
     int32_t* row = hist + (int64_t)tid * B;
-    for (int b = 0; b < B; ++b) row[b] += off;
+    int run = off;
+    for (int b0 = 0; b0 < B; b0 += 16) {
+      int c[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) c[u] = b0 + u < B ? row[b0 + u] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (b0 + u < B) {
+          row[b0 + u] = run;
+          run += c[u];
+        }
+    }
     offsets[tid] = off;
   }
   if (tid == 0) offsets[E] = s_bad ? -1 : (int32_t)R;
@@ -445,12 +452,17 @@ int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const i
 //     (ids out of [0, E) or not sorted: no tiles at all, counts[2] = 1);
 //  2. per-expert tile counts and an exclusive scan over the experts;
 //  3. each thread writes the tiles of its experts, then the padding.
+// Workgroup j builds job j's tables (two jobs: two weight shapes over the
+// same sorted ids in one launch).
 __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restrict__ ids,
                                                           const int32_t* __restrict__ offs, int64_t R, int E,
-                                                          int N, int limit, int VR, int BM, int BN,
-                                                          int4* __restrict__ qmv_tab, int qmv_cap,
-                                                          int4* __restrict__ qmm_tab, int qmm_cap,
-                                                          int32_t* __restrict__ counts) {
+                                                          TileTableJob j0, TileTableJob j1) {
+  const TileTableJob& job = blockIdx.x == 0 ? j0 : j1;
+  const int N = job.N, limit = job.limit, VR = job.VR, BM = job.BM, BN = job.BN;
+  int4* __restrict__ qmv_tab = job.qmv_tab;
+  int4* __restrict__ qmm_tab = job.qmm_tab;
+  const int qmv_cap = job.qmv_cap, qmm_cap = job.qmm_cap;
+  int32_t* __restrict__ counts = job.counts;
   extern __shared__ int tt_smem[];
   int* rstart = tt_smem;      // [E] first index of expert e's run
   int* rend = tt_smem + E;    // [E] one past its last index (0: no run)
@@ -556,15 +568,15 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   for (int t = tot_m + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
 }
 
-int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E, int N, int limit,
-                      int VR, int BM, int BN, int4* qmv_tab, int qmv_cap, int4* qmm_tab, int qmm_cap,
-                      int32_t* counts) {
+int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E,
+                      const TileTableJob* jobs, int njobs) {
   if (E > kTileTableMaxExperts)
     return set_error(LISAQ_EUNSUPPORTED, "gather_qmm: E=%d experts (at most %d)", E, kTileTableMaxExperts);
+  if (njobs < 1 || njobs > 2) return set_error(LISAQ_EINVAL_SHAPE, "gather_tile_table: %d jobs", njobs);
   const int lds = 2 * E * 4;
   if (int rc = allow_dyn_lds((const void*)tile_table_kernel, lds, "gather_tile_table")) return rc;
-  hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(1024), lds, st, ids, offs, R, E, N, limit, VR, BM, BN,
-                     qmv_tab, qmv_cap, qmm_tab, qmm_cap, counts);
+  hipLaunchKernelGGL(tile_table_kernel, dim3(njobs), dim3(1024), lds, st, ids, offs, R, E, jobs[0],
+                     jobs[njobs - 1]);
   return check_launch("gather_tile_table");
 }
 
