@@ -152,16 +152,28 @@ static int run_qmm(hipStream_t st, const void* x, const uint32_t* w, const void*
   return qmm_launch(st, c, p, bits, gs, c.grid, 1, ws, ws_bytes);
 }
 
-// Gather workspace layout: [counts 256 B][qmv table][qmm table], 256-B aligned.
-struct GatherLayout {
-  int limit, Mmax, qmv_cap, qmm_cap;
-  int qmv_grid;  // matvec launch grid (qmv_cap, or a short grid walking the table)
-  size_t qmv_off, qmm_off, total;
+// Gather workspace layout: [counts 256 B][matvec table 0][matvec table 1]
+// [qmm table], 256-B aligned.  Matvec class 0 takes the runs of at most mv[0].M
+// rows (a kernel sized for them stages all of K at once), class 1 (present when
+// runs of mv[0].M < len < limit can occur) the longer ones.
+struct GatherMv {
+  int M;     // rows of x the kernel is sized for
+  int cap;   // table entries (0: class absent)
+  int grid;  // launch grid (cap, or a short grid walking the table)
+  size_t off;
   QmvConfig qc;
+};
+struct GatherLayout {
+  int limit, Mmax, qmm_cap;
+  GatherMv mv[2];
+  size_t qmm_off, total;
   QmmConfig mc;
 };
 
 static size_t up256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Rows of x of the short-run matvec class (runs up to this length)
+constexpr int kGatherMvRows = 16;
 
 // max_run: an upper bound of the longest run of equal ids when the caller
 // knows one (moe_forward: a token picks an expert at most once, so T);
@@ -176,7 +188,40 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   const int64_t mr = (max_run > 0 && max_run < R) ? max_run : R;
   L.Mmax = (int)((mr < L.limit - 1) ? mr : L.limit - 1);
   if (L.Mmax < 1) L.Mmax = 1;
-  L.qc = qmv_config(L.Mmax, N, K, gs, bits, /*single_pass=*/true);
+  int mv = tune_int("LISAQ_GATHER_MV_ROWS", kGatherMvRows);
+  if (mv < 1) mv = 1;
+  L.mv[0].M = L.Mmax < mv ? L.Mmax : mv;
+  L.mv[1].M = L.Mmax > mv ? L.Mmax : 0;
+  const int64_t avg = R / (runs > 0 ? runs : 1);  // average run length
+  size_t o = 256;
+  for (int j = 0; j < 2; ++j) {
+    GatherMv& c = L.mv[j];
+    if (c.M == 0) {
+      c.qc.tile_rows = 16;
+      continue;
+    }
+    c.qc = qmv_config(c.M, N, K, gs, bits, /*single_pass=*/true);
+    if (c.qc.kind == 2) {
+      // streaming matvec over a table: a wave per 16-row tile and 4 tiles per
+      // block (each wave all of K for its rows, no reduction between waves;
+      // the block's x staged once for 64 rows of W)
+      int nw = tune_int("LISAQ_GATHER_MV_NW", 1), tpb = tune_int("LISAQ_GATHER_MV_TPB", 4);
+      if (!(nw == 1 || nw == 2 || nw == 4 || nw == 8)) nw = 1;
+      if (tpb < 1 || nw * tpb > 8) tpb = 8 / nw;
+      c.qc = qmvt_table_config(c.qc, gs, c.M, bits, nw, tpb);
+    }
+    c.cap = (int)(runs * ((N + c.qc.tile_rows - 1) / c.qc.tile_rows));
+    // The streaming matvec walks its table with a short grid where the class
+    // is expected to be sparse (a block per entry would mostly dispatch
+    // blocks that find no tile, ~10 us per 16K blocks): class 0 when runs
+    // average over 4 x its rows, class 1 when they average at most half of
+    // class 0's rows or at least 4 x the limit.
+    const bool sparse = j == 0 ? avg > 4 * (int64_t)L.mv[0].M
+                               : (2 * avg <= L.mv[0].M || avg >= 4 * (int64_t)L.limit);
+    c.grid = (c.qc.kind == 2 && sparse && c.cap > kQmvtWalkGrid) ? kQmvtWalkGrid : c.cap;
+    c.off = o;
+    o += up256((size_t)c.cap * 16);
+  }
   L.mc = qmm_config(L.limit, N, K, gs, bits);
   {
     const int mt = tall ? 8 : tune_int("LISAQ_GATHER_MT", L.mc.MT);
@@ -185,15 +230,8 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
       L.mc.BM = 32 * mt;
     }
   }
-  L.qmv_cap = (int)(runs * ((N + L.qc.tile_rows - 1) / L.qc.tile_rows));
   L.qmm_cap = (mr >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
-  // Runs averaging >= 4x the matvec limit leave few (usually no) runs to the
-  // matvec: a block per table entry would spend ~10 us dispatching blocks that
-  // find no tile, so a short grid walks the table instead.
-  L.qmv_grid = L.qmv_cap;
-  if (L.qc.kind == 2 && R >= 4 * (int64_t)L.limit * E && L.qmv_cap > kQmvtWalkGrid) L.qmv_grid = kQmvtWalkGrid;
-  L.qmv_off = 256;
-  L.qmm_off = L.qmv_off + up256((size_t)L.qmv_cap * 16);
+  L.qmm_off = o;
   L.total = L.qmm_off + up256((size_t)L.qmm_cap * 16);
   return L;
 }
@@ -201,8 +239,22 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
 // Tile tables of a gather (runs of the sorted ids) into the workspace.
 static TileTableJob gather_job(const GatherLayout& L, int64_t N, void* ws) {
   char* base = (char*)ws;
-  return TileTableJob{(int)N, L.limit, L.qc.tile_rows, L.mc.BM, L.mc.BN, (int4*)(base + L.qmv_off), L.qmv_cap,
-                      (int4*)(base + L.qmm_off), L.qmm_cap, (int32_t*)base};
+  TileTableJob j{};
+  j.N = (int)N;
+  j.limit = L.limit;
+  j.MV = L.mv[0].M;
+  j.BM = L.mc.BM;
+  j.BN = L.mc.BN;
+  for (int c = 0; c < 2; ++c) {
+    j.mv_tab[c] = L.mv[c].cap ? (int4*)(base + L.mv[c].off) : nullptr;
+    j.mv_cap[c] = L.mv[c].cap;
+    j.mv_pad[c] = L.mv[c].grid;
+    j.mv_vr[c] = L.mv[c].qc.tile_rows;
+  }
+  j.qmm_tab = (int4*)(base + L.qmm_off);
+  j.qmm_cap = L.qmm_cap;
+  j.counts = (int32_t*)base;
+  return j;
 }
 static int gather_tables(hipStream_t st, const GatherLayout& L, const int32_t* rhs, int64_t R, int64_t N, int E,
                          void* ws, const int32_t* offs = nullptr) {
@@ -216,22 +268,24 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
                          const void* b, void* y, int64_t R, int64_t N, int64_t K, int gs, int bits, void* ws) {
   char* base = (char*)ws;
   int rc;
-  if (L.qmv_cap > 0) {
+  for (int j = 0; j < 2; ++j) {
+    const GatherMv& c = L.mv[j];
+    if (c.cap == 0) continue;
     QmvParams p{};
     p.x = (const uint16_t*)x;
     p.w = w;
     p.s = (const uint16_t*)s;
     p.b = (const uint16_t*)b;
     p.y = (uint16_t*)y;
-    p.tiles = (const int4*)(base + L.qmv_off);
-    p.M = L.Mmax;
+    p.tiles = (const int4*)(base + c.off);
+    p.M = c.M;
     p.N = (int)N;
     p.K = (int)K;
     p.G = (int)(K / gs);
     p.part_rows = (int)R;
-    p.tile_cap = L.qmv_cap;
-    p.tile_stride = L.qmv_grid < L.qmv_cap ? L.qmv_grid : 0;
-    rc = qmv_launch(st, L.qc, p, bits, gs, L.qmv_grid);
+    p.tile_cap = c.cap;
+    p.tile_stride = c.grid < c.cap ? c.grid : 0;
+    rc = qmv_launch(st, c.qc, p, bits, gs, c.grid);
     if (rc) return rc;
   }
   if (L.qmm_cap > 0) {
@@ -618,8 +672,17 @@ static bool moe_gu_path(int64_t T, int64_t H, int64_t I, int E, int k, int gs, i
 // The gate|up matmul's tile table: {cap entries at ws + 256, counts at ws}
 static TileTableJob gu_job(int64_t R, int64_t I, int E, void* ws) {
   char* gb = (char*)ws;
-  return TileTableJob{(int)I, /*limit=*/1, 16, qmm_gu_rows(R, E), kGuBN, nullptr, 0, (int4*)(gb + 256),
-                      (int)gu_cap(R, I, E), (int32_t*)gb};
+  TileTableJob j{};
+  j.N = (int)I;
+  j.limit = 1;  // every run as matmul tiles
+  j.MV = 1;
+  j.BM = qmm_gu_rows(R, E);
+  j.BN = kGuBN;
+  j.mv_vr[0] = j.mv_vr[1] = 16;
+  j.qmm_tab = (int4*)(gb + 256);
+  j.qmm_cap = (int)gu_cap(R, I, E);
+  j.counts = (int32_t*)gb;
+  return j;
 }
 
 // Gate|up + SwiGLU over sorted rows: tile table (from the expert offsets

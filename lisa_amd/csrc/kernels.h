@@ -32,13 +32,17 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, in
 int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* w, const void* s, const void* b,
                     void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype);
 constexpr int kTileTableMaxExperts = 16384;
-// One set of gather tile tables: N output rows per expert, runs shorter
-// than `limit` as matvec tiles of VR rows, the others as BM x BN matmul tiles;
-// counts[0..2]: matvec tiles, matmul tiles, overflow/bad-ids flag.
+// One set of gather tile tables: N output rows per expert; runs shorter than
+// `limit` as matvec tiles, of mv_vr[0] output rows in table mv_tab[0] when
+// they hold at most MV rows, else of mv_vr[1] rows in mv_tab[1]; the others as
+// BM x BN matmul tiles.  Entries past a matvec table's count are written as
+// {-1,..} for mv_pad[j] entries (its launch grid), the matmul table's up to
+// its capacity.  counts[0..2]: matvec tiles, matmul tiles, overflow/bad-ids
+// flag.
 struct TileTableJob {
-  int N, limit, VR, BM, BN;
-  int4* qmv_tab;
-  int qmv_cap;
+  int N, limit, MV, BM, BN;
+  int4* mv_tab[2];
+  int mv_cap[2], mv_pad[2], mv_vr[2];
   int4* qmm_tab;
   int qmm_cap;
   int32_t* counts;

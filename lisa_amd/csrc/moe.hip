@@ -444,7 +444,9 @@ int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const i
 // ---------------------------------------------------------------------------
 // gather_qmm tile tables.  The sorted expert ids form one run per expert; each
 // run becomes either matvec tiles (run length < limit: {e, start, len, n tile
-// of VR rows}) or matmul tiles ({e, start + i*BM, rows, n tile of BN}),
+// of VR rows}, in one of two tables by run length, <= MV rows or longer, for
+// matvec kernels sized for each) or matmul tiles ({e, start + i*BM, rows, n
+// tile of BN}),
 // matching the reference's per-run quantized_matmul dispatch.  Unused entries
 // up to each table's capacity are written as {-1,..} so a grid of `capacity`
 // workgroups can be launched without a host round trip.  One workgroup:
@@ -458,15 +460,14 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
                                                           const int32_t* __restrict__ offs, int64_t R, int E,
                                                           TileTableJob j0, TileTableJob j1) {
   const TileTableJob& job = blockIdx.x == 0 ? j0 : j1;
-  const int N = job.N, limit = job.limit, VR = job.VR, BM = job.BM, BN = job.BN;
-  int4* __restrict__ qmv_tab = job.qmv_tab;
+  const int N = job.N, limit = job.limit, MV = job.MV, BM = job.BM, BN = job.BN;
   int4* __restrict__ qmm_tab = job.qmm_tab;
-  const int qmv_cap = job.qmv_cap, qmm_cap = job.qmm_cap;
+  const int qmm_cap = job.qmm_cap;
   int32_t* __restrict__ counts = job.counts;
   extern __shared__ int tt_smem[];
   int* rstart = tt_smem;      // [E] first index of expert e's run
   int* rend = tt_smem + E;    // [E] one past its last index (0: no run)
-  __shared__ int s_q[16], s_m[16], s_bad;
+  __shared__ int s_tot[3][16], s_bad;
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += 1024) rstart[e] = rend[e] = 0;
   if (tid == 0) s_bad = 0;
@@ -504,68 +505,82 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
     }
   }
   __syncthreads();
-  const int nt32 = (N + VR - 1) / VR;  // matvec tiles per run
+  // per-thread tile counts of its experts: matvec class 0 (runs of at most MV
+  // rows), matvec class 1 (longer runs below the limit), matmul
+  const int nv0 = (N + job.mv_vr[0] - 1) / job.mv_vr[0];
+  const int nv1 = (N + job.mv_vr[1] - 1) / job.mv_vr[1];
   const int ntbn = (N + BN - 1) / BN;
   const int chunk = (E + 1023) / 1024;
   const int e0 = tid * chunk, e1 = e0 + chunk < E ? e0 + chunk : E;
-  int cq = 0, cm = 0;
+  int c[3] = {0, 0, 0};
   for (int e = e0; e < e1; ++e) {
     const int len = rend[e] - rstart[e];
     if (len <= 0) continue;
-    if (len < limit) cq += nt32;
-    else cm += (len + BM - 1) / BM * ntbn;
+    if (len >= limit) c[2] += (len + BM - 1) / BM * ntbn;
+    else if (len <= MV) c[0] += nv0;
+    else c[1] += nv1;
   }
   // inclusive scan of the per-thread counts: within each wave by shuffles,
   // then the 16 wave totals
   const int lane = tid & 63, wv = tid >> 6;
-  int iq = cq, im = cm;
+  int inc[3] = {c[0], c[1], c[2]};
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    const int aq = __shfl_up(iq, d), am = __shfl_up(im, d);
-    if (lane >= d) {
-      iq += aq;
-      im += am;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int a = __shfl_up(inc[j], d);
+      if (lane >= d) inc[j] += a;
     }
   }
   if (lane == 63) {
-    s_q[wv] = iq;
-    s_m[wv] = im;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) s_tot[j][wv] = inc[j];
   }
   __syncthreads();
-  int bq = 0, bm = 0;
-  for (int w2 = 0; w2 < wv; ++w2) {
-    bq += s_q[w2];
-    bm += s_m[w2];
-  }
-  int tq = 0, tm = 0;
-  for (int w2 = 0; w2 < 16; ++w2) {
-    tq += s_q[w2];
-    tm += s_m[w2];
-  }
+  int before[3] = {0, 0, 0}, tot[3] = {0, 0, 0};
+  for (int w2 = 0; w2 < 16; ++w2)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      if (w2 < wv) before[j] += s_tot[j][w2];
+      tot[j] += s_tot[j][w2];
+    }
   const bool bad = s_bad != 0;
-  const int tot_q = bad ? 0 : tq, tot_m = bad ? 0 : tm;
+  const int caps[3] = {job.mv_cap[0], job.mv_cap[1], qmm_cap};
+  if (bad) tot[0] = tot[1] = tot[2] = 0;
   if (tid == 0) {
-    counts[0] = tot_q;
-    counts[1] = tot_m;
-    counts[2] = (bad || tot_q > qmv_cap || tot_m > qmm_cap) ? 1 : 0;
+    counts[0] = tot[0] + tot[1];
+    counts[1] = tot[2];
+    counts[2] = (bad || tot[0] > caps[0] || tot[1] > caps[1] || tot[2] > caps[2]) ? 1 : 0;
   }
   if (!bad) {
-    int oq = bq + iq - cq, om = bm + im - cm;
+    int o[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) o[j] = before[j] + inc[j] - c[j];
     for (int e = e0; e < e1; ++e) {
       const int st = rstart[e], len = rend[e] - st;
       if (len <= 0) continue;
-      if (len < limit) {
-        for (int nt = 0; nt < nt32; ++nt, ++oq)
-          if (oq < qmv_cap) qmv_tab[oq] = make_int4(e, st, len, nt);
-      } else {
+      if (len >= limit) {
         for (int r0 = 0; r0 < len; r0 += BM)
-          for (int nt = 0; nt < ntbn; ++nt, ++om)
-            if (om < qmm_cap) qmm_tab[om] = make_int4(e, st + r0, len - r0 < BM ? len - r0 : BM, nt);
+          for (int nt = 0; nt < ntbn; ++nt, ++o[2])
+            if (o[2] < qmm_cap) qmm_tab[o[2]] = make_int4(e, st + r0, len - r0 < BM ? len - r0 : BM, nt);
+      } else if (len <= MV) {
+        for (int nt = 0; nt < nv0; ++nt, ++o[0])
+          if (o[0] < caps[0]) job.mv_tab[0][o[0]] = make_int4(e, st, len, nt);
+      } else {
+        for (int nt = 0; nt < nv1; ++nt, ++o[1])
+          if (o[1] < caps[1]) job.mv_tab[1][o[1]] = make_int4(e, st, len, nt);
       }
     }
   }
-  for (int t = tot_q + tid; t < qmv_cap; t += 1024) qmv_tab[t] = make_int4(-1, 0, 0, 0);
-  for (int t = tot_m + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
+  // padding: entries [count, count + pad) as {-1,..} (pad = the launch grid:
+  // a block whose first entry is past the count finds it empty, and a block
+  // walking the table with the grid as stride stops at the first empty one)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int hi = tot[j] + job.mv_pad[j] < caps[j] ? tot[j] + job.mv_pad[j] : caps[j];
+    for (int t = tot[j] + tid; t < hi; t += 1024) job.mv_tab[j][t] = make_int4(-1, 0, 0, 0);
+  }
+  for (int t = tot[2] + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
 }
 
 int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E,

@@ -72,6 +72,9 @@ bool qmvt_supported(int64_t M, int64_t K, int gs, int bits);
 QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool allow_split = true);
 int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);
 int qmvt_lds_bytes(const QmvConfig& c, int gs, int M, int bits);
+// a streaming-matvec configuration for tile-table launches: NW waves per
+// 16-row tile, tpb tiles per block (one table entry = 16 * tpb rows)
+QmvConfig qmvt_table_config(QmvConfig c, int gs, int M, int bits, int NW, int tpb);
 bool qmvd_supported(int64_t M, int64_t N, int64_t K, int gs, int bits);
 QmvConfig qmvd_config(int64_t M, int64_t N, int64_t K, int gs, int bits);
 int qmvd_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);

@@ -169,7 +169,7 @@ __device__ __forceinline__ void qmvt_tile(const QmvParams& p, int bx) {
     x += (int64_t)t.y * p.K;
     y += (int64_t)t.y * p.N;
     M = t.z;
-    n0 = t.w * 16;
+    n0 = (t.w * tpb + wt) * 16;  // (an entry covers tpb 16-row tiles)
   }
   const int n = n0 + col;
   const int SG = p.slab_groups;
@@ -545,6 +545,16 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   return c;
 }
 
+QmvConfig qmvt_table_config(QmvConfig c, int gs, int M, int bits, int NW, int tpb) {
+  c.NW = NW;
+  c.tpb = tpb;
+  c.S = 1;
+  c.tile_rows = 16 * tpb;
+  c.lds_bytes = qmvt_layout(c.slab_groups, gs, M, c.MQ, bits, NW * tpb, c.U).total;
+  c.ws_bytes = 0;
+  return c;
+}
+
 int qmvt_lds_bytes(const QmvConfig& c, int gs, int M, int bits) {
   return qmvt_layout(c.slab_groups, gs, M, c.MQ, bits, c.NW * (c.tpb > 0 ? c.tpb : 1), c.U).total;
 }
@@ -554,6 +564,8 @@ typedef void (*qmvt_fn)(QmvParams);
 template <int BITS, int GS, int MQ, int MR, int SB>
 static qmvt_fn pick_nw(int NW, bool walk) {
   constexpr int D = (MQ == 1) ? (SB == 256 ? 2 : 3) : 2;
+  if (NW == 1) return walk ? qmvt_walk_kernel<BITS, GS, MQ, MR, SB, 1, D> : qmvt_kernel<BITS, GS, MQ, MR, SB, 1, D>;
+  if (NW == 2) return walk ? qmvt_walk_kernel<BITS, GS, MQ, MR, SB, 2, D> : qmvt_kernel<BITS, GS, MQ, MR, SB, 2, D>;
   if (NW == 4) return walk ? qmvt_walk_kernel<BITS, GS, MQ, MR, SB, 4, D> : qmvt_kernel<BITS, GS, MQ, MR, SB, 4, D>;
   if (NW == 8) return walk ? qmvt_walk_kernel<BITS, GS, MQ, MR, SB, 8, D> : qmvt_kernel<BITS, GS, MQ, MR, SB, 8, D>;
   return nullptr;
@@ -588,12 +600,14 @@ int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
   p.S = p.tiles ? 1 : c.S;
   p.S_inner = c.S_inner;
   p.slab_groups = c.slab_groups;
-  // tile-table launches: one tile per block (the table gives each block its tile)
-  const int tpb = p.tiles ? 1 : (c.tpb > 0 ? c.tpb : 1);
-  int lds = c.lds_bytes;
-  if (tpb != c.tpb) lds = qmvt_layout(c.slab_groups, gs, p.M, c.MQ, bits, c.NW * tpb, c.U).total;
+  // tpb 16-row tiles per block; a tile-table launch: grid_x table entries
+  // (one block each, an entry covering tpb tiles), else grid_x tiles
+  const int tpb = c.tpb > 0 ? c.tpb : 1;
+  if (64 * c.NW * tpb > 512) return set_error(LISAQ_EINVAL_SHAPE, "qmvt: %d x %d waves per block", c.NW, tpb);
+  const int lds = qmvt_layout(c.slab_groups, gs, p.M, c.MQ, bits, c.NW * tpb, c.U).total;
   if (int rc = allow_dyn_lds((const void*)fn, lds, "qmvt")) return rc;
-  hipLaunchKernelGGL(fn, dim3((grid_x + tpb - 1) / tpb, p.S), dim3(64 * c.NW * tpb), lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(p.tiles ? grid_x : (grid_x + tpb - 1) / tpb, p.S), dim3(64 * c.NW * tpb), lds,
+                     stream, p);
   int rc = check_launch("qmvt");
   if (rc || p.S == 1) return rc;
   const int64_t MN = (int64_t)p.M * p.N;
