@@ -164,6 +164,8 @@ struct GatherMv {
   QmvConfig qc;
 };
 struct GatherLayout {
+  bool gu;     // gate|up tables: a matvec entry covers the same rows of both
+  bool gu_ok;  // (gu) the matvec classes run the gate|up streaming kernel
   int limit, Mmax, qmm_cap;
   GatherMv mv[2];
   size_t qmm_off, total;
@@ -180,9 +182,14 @@ constexpr int kGatherMvRows = 16;
 // otherwise R.  It only sizes the matvec rows and decides if matmul tiles can
 // occur; the tables still follow the actual runs.
 // tall: matmul tiles of 256 rows (runs known to average >= 192 rows).
+// gu: tables for gate|up + SwiGLU (N = I): matvec entries of half a block's
+// rows (the other half of its waves take the up weights), matmul tiles of the
+// gate|up matmul kernel.
 static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs, int bits, int64_t max_run = 0,
-                                  bool tall = false) {
+                                  bool tall = false, bool gu = false) {
   GatherLayout L{};
+  L.gu = gu;
+  L.gu_ok = gu;
   L.limit = lisaq_qmv_batch_limit(K, N);
   const int64_t runs = R < E ? R : E;
   const int64_t mr = (max_run > 0 && max_run < R) ? max_run : R;
@@ -209,6 +216,12 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
       if (!(nw == 1 || nw == 2 || nw == 4 || nw == 8)) nw = 1;
       if (tpb < 1 || nw * tpb > 8) tpb = 8 / nw;
       c.qc = qmvt_table_config(c.qc, gs, c.M, bits, nw, tpb);
+      if (gu) {
+        if (nw != 1 || tpb % 2) L.gu_ok = false;
+        c.qc.tile_rows = 16 * (tpb / 2 > 0 ? tpb / 2 : 1);
+      }
+    } else if (gu) {
+      L.gu_ok = false;
     }
     c.cap = (int)(runs * ((N + c.qc.tile_rows - 1) / c.qc.tile_rows));
     // The streaming matvec walks its table with a short grid where the class
@@ -229,6 +242,10 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
       L.mc.MT = mt;
       L.mc.BM = 32 * mt;
     }
+  }
+  if (gu) {
+    L.mc.BM = qmm_gu_rows(R, E);
+    L.mc.BN = kGuBN;
   }
   L.qmm_cap = (mr >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
   L.qmm_off = o;
@@ -302,6 +319,62 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
     p.G = (int)(K / gs);
     rc = L.mc.MT == 8 ? qmm_gather_tall_launch(st, p, bits, gs, L.qmm_cap) : qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
     if (rc) return rc;
+  }
+  return LISAQ_OK;
+}
+
+// Gate|up + SwiGLU over built gate|up tables (gather_layout(..., gu)): the
+// matvec classes through the gate|up streaming kernel, the matmul tiles
+// through the gate|up matmul kernel; x rows read through the row map xrows
+// (x has T rows).  act [R, I] receives SwiGLU(bf16 gate, bf16 up).
+static int gather_launch_gu(hipStream_t st, const GatherLayout& L, const void* x, const int32_t* xrows, int64_t T,
+                            const uint32_t* gw, const void* gsc, const void* gbi, const uint32_t* uw,
+                            const void* usc, const void* ubi, void* act, int64_t R, int64_t I, int64_t H, int gs,
+                            int bits, void* ws) {
+  char* base = (char*)ws;
+  int rc;
+  for (int j = 0; j < 2; ++j) {
+    const GatherMv& c = L.mv[j];
+    if (c.cap == 0) continue;
+    QmvParams p{};
+    p.x = (const uint16_t*)x;
+    p.xrows = xrows;
+    p.w = gw;
+    p.s = (const uint16_t*)gsc;
+    p.b = (const uint16_t*)gbi;
+    p.w2 = uw;
+    p.s2 = (const uint16_t*)usc;
+    p.b2 = (const uint16_t*)ubi;
+    p.y = (uint16_t*)act;
+    p.tiles = (const int4*)(base + c.off);
+    p.M = c.M;
+    p.N = (int)I;
+    p.K = (int)H;
+    p.G = (int)(H / gs);
+    p.part_rows = (int)R;
+    p.tile_cap = c.cap;
+    p.tile_stride = c.grid < c.cap ? c.grid : 0;
+    if ((rc = qmv_launch(st, c.qc, p, bits, gs, c.grid))) return rc;
+  }
+  if (L.qmm_cap > 0) {
+    QmmParams p{};
+    p.x = (const uint16_t*)x;
+    p.w = gw;
+    p.s = (const uint16_t*)gsc;
+    p.b = (const uint16_t*)gbi;
+    p.w2 = uw;
+    p.s2 = (const uint16_t*)usc;
+    p.b2 = (const uint16_t*)ubi;
+    p.xrows = xrows;
+    p.xrows_max = (int)(T - 1);
+    p.y = (uint16_t*)act;
+    p.tiles = (const int4*)(base + L.qmm_off);
+    p.M = (int)R;
+    p.N = (int)I;
+    p.K = (int)H;
+    p.G = (int)(H / gs);
+    p.ksplit = 1;
+    if ((rc = qmm_gu_launch(st, p, bits, gs, L.qmm_cap, L.mc.BM))) return rc;
   }
   return LISAQ_OK;
 }
@@ -830,12 +903,14 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
   L.d = take((size_t)R * H * 2);
   // the tables exactly as lisaq_moe_forward lays them out: runs of at most T
   // rows (a token picks an expert once)
-  const size_t g1 = gather_layout(R, I, H, E, gs, bits, T).total;
+  const size_t g1a = gather_layout(R, I, H, E, gs, bits, T).total;
+  const size_t g1b = gather_layout(R, I, H, E, gs, bits, T, false, /*gu=*/true).total;
+  const size_t g1 = g1a > g1b ? g1a : g1b;
   const size_t g2 = gather_layout(R, H, I, E, gs, bits, T, moe_down_tall(T, H, I, E, k, gs, bits)).total;
   const size_t g3 = 256 + up256((size_t)gu_cap(R, I, E) * 16);
-  // (the gate|up path keeps the down tables and the gate|up table side by
-  // side: both are built by one launch)
-  L.gws = take(g1 > up256(g2) + g3 ? g1 : up256(g2) + g3);
+  // (the down tables and the gate/up tables side by side: both are built by
+  // one launch)
+  L.gws = take(up256(g2) + (g1 > g3 ? g1 : g3));
   L.total = o;
   return L;
 }
@@ -907,6 +982,31 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
     if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;
     return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
   }
+  {
+    // gate|up + SwiGLU through the row map: the matvec runs in the gate|up
+    // streaming kernel, the matmul runs in the gate|up matmul kernel (both
+    // bitwise equal to gate, up and SwiGLU as three steps), no gathered x
+    const GatherLayout GU = gather_layout(R, I, H, E, gs, bits, T, false, /*gu=*/true);
+    const bool mm_ok = GU.qmm_cap == 0 || (H % 64 == 0 && I % 64 == 0 && (bits == 2 || bits == 4) &&
+                                           (gs == 32 || gs == 64 || gs == 128));
+    if (GU.gu_ok && mm_ok && T * H < ((int64_t)1 << 31) && path_int("LISAQ_MOE_GU_MV", 1) != 0) {
+      if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
+      if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
+      if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, d, R, H, I, 1, gs, bits))) return rc;
+      const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T);
+      if (DN.qmm_cap > 0 && (H % 64 || I % 64))
+        return set_error(LISAQ_EUNSUPPORTED, "moe_forward: H, I must be multiples of 64 for the matmul path");
+      const size_t gu_at = up256(DN.total);
+      void* gws_gu = (char*)gws + gu_at;
+      LISAQ_REQUIRE(gu_at + GU.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
+      const TileTableJob jobs[2] = {gather_job(DN, H, gws), gather_job(GU, I, gws_gu)};
+      if ((rc = launch_tile_table(st, sorted, offs, R, E, jobs, 2))) return rc;
+      if ((rc = gather_launch_gu(st, GU, x, rows, T, gw, gsc, gbi, uw, usc, ubi, g, R, I, H, gs, bits, gws_gu)))
+        return rc;
+      if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;
+      return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
+    }
+  }
   if ((rc = lisaq_gather_rows(st, x, rows, xs, R, H))) return rc;
   // gate and up share one set of tile tables; every run is at most T rows
   if ((rc = validate_mm("moe_forward gate", xs, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
@@ -914,14 +1014,17 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, d, R, H, I, 1, gs, bits))) return rc;
   const GatherLayout GU = gather_layout(R, I, H, E, gs, bits, T);
   const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T);
-  LISAQ_REQUIRE(GU.total <= gws_bytes && DN.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
+  // tables: the down gather's at gws, gate/up's after them, one launch
+  const size_t gu_at = up256(DN.total);
+  void* gws_gu = (char*)gws + gu_at;
+  LISAQ_REQUIRE(gu_at + GU.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
   if ((GU.qmm_cap > 0 || DN.qmm_cap > 0) && (H % 64 || I % 64))
     return set_error(LISAQ_EUNSUPPORTED, "moe_forward: H, I must be multiples of 64 for the matmul path");
-  if ((rc = gather_tables(st, GU, sorted, R, I, E, gws, offs))) return rc;
-  if ((rc = gather_launch(st, GU, xs, gw, gsc, gbi, g, R, I, H, gs, bits, gws))) return rc;
-  if ((rc = gather_launch(st, GU, xs, uw, usc, ubi, u, R, I, H, gs, bits, gws))) return rc;
+  const TileTableJob jobs[2] = {gather_job(DN, H, gws), gather_job(GU, I, gws_gu)};
+  if ((rc = launch_tile_table(st, sorted, offs, R, E, jobs, 2))) return rc;
+  if ((rc = gather_launch(st, GU, xs, gw, gsc, gbi, g, R, I, H, gs, bits, gws_gu))) return rc;
+  if ((rc = gather_launch(st, GU, xs, uw, usc, ubi, u, R, I, H, gs, bits, gws_gu))) return rc;
   if ((rc = lisaq_swiglu(st, g, u, g, R * I))) return rc;
-  if ((rc = gather_tables(st, DN, sorted, R, H, E, gws, offs))) return rc;
   if ((rc = gather_launch(st, DN, g, dw, dsc, dbi, d, R, H, I, gs, bits, gws))) return rc;
   return lisaq_moe_combine(st, d, wts, inv, out, T, k, H);
 }

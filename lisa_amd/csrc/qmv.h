@@ -13,6 +13,15 @@ struct QmvParams {
   const uint16_t* s;     // [(E,) N, G] bf16
   const uint16_t* b;     // [(E,) N, G] bf16
   uint16_t* y;           // [rows, N] bf16
+  // gate|up (streaming matvec over a table, one wave per tile): the second
+  // half of a block's tiles take these weights for the same output rows, and
+  // y = SwiGLU(bf16 gate, bf16 up)
+  const uint32_t* w2;
+  const uint16_t* s2;
+  const uint16_t* b2;
+  // table launches: row m of a tile is x row xrows[row start + m] (null: row
+  // start + m)
+  const int32_t* xrows;
   float* partial;        // [S, part_rows, N] f32 (split-K only)
   const int4* tiles;     // gather: {expert, row start, rows, n tile} per block, or null
   int tile_cap;          // gather: table entries

@@ -20,6 +20,7 @@
 // permuted order of the unpacked codes; scales/biases are staged as f32
 // pairs.  No workgroup barrier is needed in the main loop.
 #include "lisaq_common.h"
+#include "moe_dev.h"
 #include "qmv.h"
 
 #include <cstdio>
@@ -152,13 +153,19 @@ __device__ __forceinline__ void qmvt_tile(const QmvParams& p, int bx) {
   const int col = lane & 15;  // row n of the tile / row m of x in the A operand
   const int q = lane >> 4;    // lane group
 
-  const uint32_t* w = p.w;
-  const uint16_t* sc = p.s;
-  const uint16_t* bi = p.b;
+  // gate|up (table launches, NW == 1, tpb even): tiles [0, tpb/2) of the
+  // block take the gate weights, the others the up weights for the same rows
+  const bool gu = p.w2 != nullptr;
+  const int th = gu ? tpb / 2 : tpb;  // tiles per weight set
+  const bool upw = gu && wt >= th;
+  const uint32_t* w = upw ? p.w2 : p.w;
+  const uint16_t* sc = upw ? p.s2 : p.s;
+  const uint16_t* bi = upw ? p.b2 : p.b;
   const uint16_t* x = p.x;
   uint16_t* y = p.y;
   int n0 = (bx * tpb + wt) * 16;
   int M = p.M;
+  int xrow = 0;  // (row map) this lane's x row: lane m holds row m's index
   if (p.tiles) {
     const int4 t = p.tiles[bx];
     if (t.x < 0) return;
@@ -166,10 +173,11 @@ __device__ __forceinline__ void qmvt_tile(const QmvParams& p, int bx) {
     w += e * (int64_t)p.N * (p.K / PACK);
     sc += e * (int64_t)p.N * p.G;
     bi += e * (int64_t)p.N * p.G;
-    x += (int64_t)t.y * p.K;
+    if (p.xrows) xrow = p.xrows[t.y + (lane < t.z ? lane : t.z - 1)];
+    else x += (int64_t)t.y * p.K;
     y += (int64_t)t.y * p.N;
     M = t.z;
-    n0 = (t.w * tpb + wt) * 16;  // (an entry covers tpb 16-row tiles)
+    n0 = (t.w * th + (upw ? wt - th : wt)) * 16;  // (an entry covers th 16-row tiles)
   }
   const int n = n0 + col;
   const int SG = p.slab_groups;
@@ -235,8 +243,9 @@ __device__ __forceinline__ void qmvt_tile(const QmvParams& p, int bx) {
         const int qq = id2 & 3;
         const int gl = (id2 >> 2) % GL;
         const int m = (id2 >> 2) / GL;
+        const int64_t xr = p.xrows ? (int64_t)__shfl(xrow, m) : (int64_t)m;
         const u32x4* src =
-            reinterpret_cast<const u32x4*>(x + (int64_t)m * p.K + (int64_t)(g_begin + gl) * GS + qq * HV);
+            reinterpret_cast<const u32x4*>(x + xr * p.K + (int64_t)(g_begin + gl) * GS + qq * HV);
 #pragma unroll
         for (int i = 0; i < HV / 8; ++i) {
           const u32x4 v = src[i];
@@ -429,6 +438,29 @@ __device__ __forceinline__ void qmvt_tile(const QmvParams& p, int bx) {
         yacc[a][ii] = v;
       }
   }
+  if (gu) {
+    // the up tiles hand their sums to the gate tiles (LDS free since the
+    // barrier above); y = SwiGLU of the bf16-rounded gate and up values
+    if (upw) {
+#pragma unroll
+      for (int a = 0; a < MQ; ++a)
+#pragma unroll
+        for (int ii = 0; ii < MR; ++ii) red[(((wt - th) * MQ + a) * 4 + ii) * 64 + lane] = yacc[a][ii];
+    }
+    __syncthreads();
+    if (upw || n >= p.N) return;
+#pragma unroll
+    for (int a = 0; a < MQ; ++a)
+#pragma unroll
+      for (int ii = 0; ii < MR; ++ii) {
+        const int m = 16 * a + 4 * q + ii;
+        if (m >= M) continue;
+        const float gv = bf2f(f2bf(yacc[a][ii]));
+        const float uv = bf2f(f2bf(red[((wt * MQ + a) * 4 + ii) * 64 + lane]));
+        y[(int64_t)m * p.N + n] = swiglu_bf16(gv, uv);
+      }
+    return;
+  }
   if (wl != 0 || n >= p.N) return;
 #pragma unroll
   for (int a = 0; a < MQ; ++a)
@@ -588,6 +620,9 @@ static qmvt_fn pick_t(int MQ, int MR, int SB, int NW, bool walk) {
 
 int qmvt_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
   const bool walk = p.tiles && p.tile_stride > 0;
+  if (p.w2 && !(p.tiles && c.NW == 1 && c.tpb >= 2 && c.tpb % 2 == 0))
+    return set_error(LISAQ_EINVAL_LAYOUT, "qmvt: gate|up needs a table launch, 1 wave per tile, an even tile count");
+  if (p.xrows && !p.tiles) return set_error(LISAQ_EINVAL_LAYOUT, "qmvt: a row map needs a table launch");
   if (walk && (grid_x != p.tile_stride || p.tile_cap <= 0))
     return set_error(LISAQ_EINVAL_LAYOUT, "qmvt: walking grid %d != stride %d", grid_x, p.tile_stride);
   qmvt_fn fn = nullptr;

@@ -186,6 +186,35 @@ def test_moe_forward_parity(dev, oracle, T):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("T,E,k,H,I,bits,gs,skew", [(16, 128, 8, 2048, 768, 4, 64, False),
+                                                    (64, 128, 8, 2048, 768, 4, 64, False),
+                                                    (64, 128, 8, 2048, 768, 4, 64, True),
+                                                    (200, 128, 8, 2048, 768, 4, 64, True),
+                                                    (40, 16, 2, 512, 320, 2, 64, True),
+                                                    (9, 8, 3, 256, 256, 4, 128, False)])
+def test_moe_forward_gate_up_matvec(dev, monkeypatch, T, E, k, H, I, bits, gs, skew):
+    """Between the decode window and the gate|up matmul path (9 <= T, T*k < 32E): gate|up + SwiGLU in
+    the gate|up streaming matvec (and the gate|up matmul for runs at or above the matvec limit; skewed
+    routing makes such runs), x read through the row map -- bitwise equal to the same block with gate,
+    up and SwiGLU as separate launches over gathered rows (LISAQ_MOE_GU_MV=0)."""
+    import torch
+
+    rng = np.random.default_rng(T * 7 + E + bits)
+    st = lambda n, kk: tuple(a.reshape(E, n, -1) for a in np_linear(rng, E * n, kk, bits, gs))
+    G, U, D = st(I, H), st(I, H), st(H, I)
+    x = np_x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    if skew:  # a few experts picked by most tokens: runs of up to T rows
+        lg[:, :3] += 4.0
+    dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(s_)) for s_ in (G, U, D)]
+    xd, lgd = to_dev_bf16(x, dev), to_dev(lg, dev)
+    fused = from_dev_bf16(ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, group_size=gs, bits=bits))
+    monkeypatch.setenv("LISAQ_MOE_GU_MV", "0")
+    steps = from_dev_bf16(ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, group_size=gs, bits=bits))
+    torch.cuda.synchronize()
+    assert np.array_equal(fused, steps)
+
+
 def _run_ref(oracle, xr, W, S, B, e, limit):
     """One run of expert e as the reference's per-run loop computes it (array_ops.rs:591-630)."""
     fn = oracle.qmv if xr.shape[0] < limit else oracle.qmm
