@@ -224,10 +224,14 @@ LISAQ_API int lisaq_moe_combine(void* stream, const void* down_sorted, const flo
  * moe.rs:263-332, 415-420) take the fused decode path of moe_decode.rs
  * (routing + gate|up + SwiGLU, then down + combine: two launches),
  * with the same rounding points; the environment variable LISAQ_MOE_FUSED=0
- * selects the generic path instead.  Many tokens (T*k >= 32*E, H % 64 == 0,
+ * selects the generic path instead.  Many tokens (T*k >= 20*E, H % 64 == 0,
  * I % 64 == 0) take lisaq_gather_qmm_swiglu for gate|up + SwiGLU (one launch,
- * x read through the sort's row map); LISAQ_MOE_GU=0 selects the three-step
- * gather, gate, up, SwiGLU sequence instead.
+ * x read through the sort's row map); LISAQ_MOE_GU=0 selects the path below.
+ * Between the two: gate|up + SwiGLU of the runs shorter than
+ * qmv_batch_limit(H, I) in one matvec launch per run-length class (matvec
+ * arithmetic), of the longer runs in the gate|up matmul, x read through the
+ * row map -- bitwise equal to the three-step gather, gate, up, SwiGLU
+ * sequence, which LISAQ_MOE_GU_MV=0 selects.
  * workspace: lisaq_moe_workspace() bytes, zero-filled before first use. */
 LISAQ_API int lisaq_moe_forward(void* stream, const void* x, const float* logits, const uint32_t* gate_w,
                       const void* gate_s, const void* gate_b, const uint32_t* up_w,

@@ -735,10 +735,13 @@ static int64_t gu_cap(int64_t R, int64_t I, int E) {
 }
 
 // The fused gate|up matmul serves the prefill when the average expert run is
-// at least 32 rows (short runs then cost one 32-row block of matrix work each).
+// at least 20 rows (short runs then cost one 32-row block of matrix work
+// each); fewer rows: the gate|up streaming matvec path (measured crossover at
+// E = 128, k = 8, H = 2048, I = 768: between T = 256 and 320).
 static bool moe_gu_path(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
   const int64_t R = T * k;
-  return path_int("LISAQ_MOE_GU", 1) != 0 && R >= 32 * (int64_t)E && H % 64 == 0 && I % 64 == 0 &&
+  return path_int("LISAQ_MOE_GU", 1) != 0 && R >= tune_int("LISAQ_MOE_GU_MIN", 20) * (int64_t)E && H % 64 == 0 &&
+         I % 64 == 0 &&
          (bits == 4 || bits == 2) && (gs == 32 || gs == 64 || gs == 128) && T * H < ((int64_t)1 << 31);
 }
 
