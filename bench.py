@@ -62,7 +62,9 @@ def main():
     ap.add_argument("--blaslt", action="store_true",
                     help="only compare the prefill matmul with dequantize-then-hipBLASLt bf16 GEMM on the same shapes")
     ap.add_argument("--moe", action="store_true",
-                    help="only time the MoE block rows (T=1 and T=4096) of the configuration table")
+                    help="only time the MoE block rows (T=1, 64, 4096) of the configuration table")
+    ap.add_argument("--moe-tokens", type=int, nargs="*", default=None,
+                    help="with --moe: only these of the MoE rows' token counts (1, 64, 4096)")
     ap.add_argument("--addnorm", action="store_true",
                     help="only time the residual add + RMSNorm matvec against the plain matvec at the north-star shape")
     args = ap.parse_args()
@@ -95,7 +97,7 @@ def main():
         addnorm_compare(dev, gen)
         return
     if args.moe:
-        for r in moe_rows(dev, gen, torch.cuda.Stream()):
+        for r in moe_rows(dev, gen, torch.cuda.Stream(), args.moe_tokens):
             print(json.dumps(r), flush=True)
         return
     M, N, K, bits, gs = 1, 17408, 5120, 4, 64
@@ -343,9 +345,10 @@ def config_table(dev, gen, stream):
     return rows
 
 
-def moe_rows(dev, gen, stream):
+def moe_rows(dev, gen, stream, only=None):
     """The MoE block rows (BASELINE config [4]): E=128, k=8, H=2048, I=768, 4-bit gs64; T=1 with rotating
-    router logits (different experts each call) and T=4096."""
+    router logits (different experts each call), T=64 (the matvec path between decode and prefill; bytes:
+    the weights of the experts the call routes to, each read once) and T=4096."""
     import torch
 
     from lisa_amd import ops
@@ -359,13 +362,17 @@ def moe_rows(dev, gen, stream):
     gate = torch_linear(I, H, 4, gs, device=dev, generator=gen, experts=E)
     up = torch_linear(I, H, 4, gs, device=dev, generator=gen, experts=E)
     down = torch_linear(H, I, 4, gs, device=dev, generator=gen, experts=E)
-    for T, n_logits, steps in ((1, 32, 100), (4096, 1, 5)):
+    for T, n_logits, steps in ((1, 32, 100), (64, 8, 40), (4096, 1, 5)):
+        if only and T not in only:
+            continue
         x = torch_x(T, H, device=dev, generator=gen)
         logits = [torch.randn(T, E, device=dev, generator=gen) for _ in range(n_logits)]
         t = _time_graph(stream, lambda i: ops.moe_forward(x, logits[i % n_logits], gate, up, down, k), n_logits, steps)
         per_expert = 3 * (I * H // 2 + 2 * 2 * I * (H // gs))  # packed W + scales + biases of one expert's 3 matrices
-        if T == 1:
-            nb = k * per_expert
+        if T <= 64:
+            # distinct experts per call, averaged over the logit sets
+            used = sum(int(torch.unique(ops.moe_route(lg, k)[0]).numel()) for lg in logits) / n_logits
+            nb = int(round(used * per_expert))
             rows.append({"workload": "MoE 4-bit E=128 k=8 (routed block: route, sort, gate|up + SwiGLU, down, combine)", "T": T,
                          "us": round(t * 1e6, 2), "value": round(nb / t / 1e9, 1), "unit": "GB/s",
                          "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nb})

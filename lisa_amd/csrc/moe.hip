@@ -167,57 +167,87 @@ __global__ __launch_bounds__(256) void sort_count_kernel(const int32_t* __restri
   for (int e = tid; e <= E; e += 256) hist[(int64_t)e * B + b] = cnt[e];
 }
 
+// hist [E+1][B] per-block counts -> each block's first position per expert
+// (in place), offsets [E+1].  TPE = 1024 / (E + 1) rounded down to a power of
+// two threads share an expert row (row E: the invalid ids): each sums a
+// contiguous slice of the row, the slices are scanned within the group by
+// shuffles, the expert totals across the experts through LDS; then each
+// thread writes its slice's positions.
 __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ hist, int B, int E, int64_t R,
                                                          int32_t* __restrict__ offsets) {
-  __shared__ int wsum[16], s_bad;
+  __shared__ int wsum[16];
+  __shared__ int tot[1025];  // expert totals, then their exclusive prefix
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  // per expert: exclusive prefix over the blocks (16 loads in flight at a time)
-  auto row_sum = [&](const int32_t* row) {
-    int t = 0;
-    for (int b0 = 0; b0 < B; b0 += 16) {
+  int tpe = 1;
+  while (tpe * 2 * (E + 1) <= 1024 && tpe * 2 <= 64) tpe *= 2;
+  const int e = tid / tpe, part = tid % tpe;  // expert row, slice of it
+  const int per = (B + tpe - 1) / tpe;
+  const int b0 = part * per, b1 = b0 + per < B ? b0 + per : B;
+  const bool active = e <= E;
+  int32_t* row = hist + (int64_t)(active ? e : 0) * B;
+  // slice sum (16 loads in flight at a time)
+  int slice = 0;
+  if (active)
+    for (int b = b0; b < b1; b += 16) {
       int c[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) c[u] = b0 + u < B ? row[b0 + u] : 0;
+      for (int u = 0; u < 16; ++u) c[u] = b + u < b1 ? row[b + u] : 0;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) t += c[u];
+      for (int u = 0; u < 16; ++u) slice += c[u];
     }
-    return t;
-  };
-  if (tid == 0) s_bad = row_sum(hist + (int64_t)E * B);  // invalid ids (row E)
-  // (pass 1 reads the expert's row for its total; pass 2, after the scan over
-  // the experts, reads it again and writes the final positions: no
-  // read-after-write chains through memory)
-  const int total = tid < E ? row_sum(hist + (int64_t)tid * B) : 0;
-  // exclusive scan of the expert totals (E <= 1024: one per thread)
-  const int mine = tid < E ? total : 0;
-  int inc = mine;
+  // exclusive scan of the slices within the expert's group (tpe lanes, aligned)
+  int inc = slice;
+  for (int d = 1; d < tpe; d <<= 1) {
+    const int a = __shfl_up(inc, d, tpe);
+    if (part >= d) inc += a;
+  }
+  const int total = __shfl(inc, tpe - 1, tpe);  // the expert's total
+  if (active && part == 0) tot[e] = total;
+  if (E >= 1024 && tid == 0) {  // (E = 1024: no thread left for row E)
+    const int32_t* rowE = hist + (int64_t)E * B;
+    int nb = 0;
+    for (int b = 0; b < B; b += 16) {
+      int c[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) c[u] = b + u < B ? rowE[b + u] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) nb += c[u];
+    }
+    tot[E] = nb;
+  }
+  __syncthreads();
+  // exclusive scan of the expert totals 0..E-1 (one per thread), as before
+  const int mine = tid < E ? tot[tid] : 0;
+  int ex = mine;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    const int a = __shfl_up(inc, d);
-    if (lane >= d) inc += a;
+    const int a = __shfl_up(ex, d);
+    if (lane >= d) ex += a;
   }
-  if (lane == 63) wsum[wv] = inc;
+  if (lane == 63) wsum[wv] = ex;
   __syncthreads();
   int base = 0;
   for (int w2 = 0; w2 < wv; ++w2) base += wsum[w2];
-  const int off = base + inc - mine;
-  if (tid < E) {
-    int32_t* row = hist + (int64_t)tid * B;
-    int run = off;
-    for (int b0 = 0; b0 < B; b0 += 16) {
+  const int bad = tot[E];
+  __syncthreads();
+  if (tid < E) tot[tid] = base + ex - mine;
+  __syncthreads();
+  if (active && e < E) {
+    int run = tot[e] + inc - slice;  // first position of the slice
+    for (int b = b0; b < b1; b += 16) {
       int c[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) c[u] = b0 + u < B ? row[b0 + u] : 0;
+      for (int u = 0; u < 16; ++u) c[u] = b + u < b1 ? row[b + u] : 0;
 #pragma unroll
       for (int u = 0; u < 16; ++u)
-        if (b0 + u < B) {
-          row[b0 + u] = run;
+        if (b + u < b1) {
+          row[b + u] = run;
           run += c[u];
         }
     }
-    offsets[tid] = off;
+    if (part == 0) offsets[e] = tot[e];
   }
-  if (tid == 0) offsets[E] = s_bad ? -1 : (int32_t)R;
+  if (tid == 0) offsets[E] = bad ? -1 : (int32_t)R;
 }
 
 __global__ __launch_bounds__(256) void sort_scatter_kernel(const int32_t* __restrict__ ids, int64_t R, int E,

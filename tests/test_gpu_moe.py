@@ -295,17 +295,18 @@ def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
     assert_close_bf16(outs["1"][0], bf16_bits_to_f32(outs["0"][0]), what=f"fused vs generic T={T} k={k} bits={bits}")
 
 
-def test_moe_forward_generic_equals_composition(dev, monkeypatch):
+@pytest.mark.parametrize("T,E,k,H,I", [(600, 64, 8, 128, 64), (40, 1024, 4, 256, 128), (50, 1023, 2, 256, 128)])
+def test_moe_forward_generic_equals_composition(dev, monkeypatch, T, E, k, H, I):
     """moe_forward's generic path (multi-workgroup counting sort, tile tables
     built from the expert offsets) against the same steps composed from the
     public entry points (one-workgroup sort, tile tables from the sorted ids):
     bit-identical, at a size where the sort spans several workgroups
-    (T=600, k=8: 4800 ids)."""
+    (T=600, k=8: 4800 ids), and at E = 1024 / 1023 experts (the sort's scan
+    with one thread per expert row)."""
     import torch
 
     monkeypatch.setenv("LISAQ_MOE_FUSED", "0")
-    rng = np.random.default_rng(600)
-    T, E, k, H, I = 600, 64, 8, 128, 64
+    rng = np.random.default_rng(T + E)
     G, U, D = _expert_stack(rng, E, I, H), _expert_stack(rng, E, I, H), _expert_stack(rng, E, H, I)
     x = to_dev_bf16(np_x(rng, T, H), dev)
     lg = to_dev(rng.standard_normal((T, E)).astype(np.float32), dev)
