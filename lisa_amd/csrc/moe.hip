@@ -168,55 +168,43 @@ __global__ __launch_bounds__(256) void sort_count_kernel(const int32_t* __restri
 }
 
 // hist [E+1][B] per-block counts -> each block's first position per expert
-// (in place), offsets [E+1].  TPE = 1024 / (E + 1) rounded down to a power of
-// two threads share an expert row (row E: the invalid ids): each sums a
-// contiguous slice of the row, the slices are scanned within the group by
-// shuffles, the expert totals across the experts through LDS; then each
-// thread writes its slice's positions.
+// (in place), offsets [E+1].  Wave w takes the rows w, w + 16, ... (row E:
+// the invalid ids), 64 blocks of a row per load (coalesced), the loads of 8
+// rows issued before any is used: pass 1 the row totals, then the exclusive
+// scan of the expert totals, pass 2 each row's prefix over its blocks by a
+// wave scan, written back in place.
 __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ hist, int B, int E, int64_t R,
                                                          int32_t* __restrict__ offsets) {
+  constexpr int RB = 8;  // rows per batch of loads
   __shared__ int wsum[16];
-  __shared__ int tot[1025];  // expert totals, then their exclusive prefix
+  __shared__ int tot[1025];  // row totals, then the experts' first positions
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  int tpe = 1;
-  while (tpe * 2 * (E + 1) <= 1024 && tpe * 2 <= 64) tpe *= 2;
-  const int e = tid / tpe, part = tid % tpe;  // expert row, slice of it
-  const int per = (B + tpe - 1) / tpe;
-  const int b0 = part * per, b1 = b0 + per < B ? b0 + per : B;
-  const bool active = e <= E;
-  int32_t* row = hist + (int64_t)(active ? e : 0) * B;
-  // slice sum (16 loads in flight at a time)
-  int slice = 0;
-  if (active)
-    for (int b = b0; b < b1; b += 16) {
-      int c[16];
+  // pass 1: row totals
+  for (int r0 = wv; r0 <= E; r0 += 16 * RB) {
+    int acc[RB];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) c[u] = b + u < b1 ? row[b + u] : 0;
+    for (int i = 0; i < RB; ++i) acc[i] = 0;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      int v[RB];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) slice += c[u];
+      for (int i = 0; i < RB; ++i) {
+        const int r = r0 + 16 * i;
+        v[i] = (r <= E && b0 + lane < B) ? hist[(int64_t)r * B + b0 + lane] : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) acc[i] += v[i];
     }
-  // exclusive scan of the slices within the expert's group (tpe lanes, aligned)
-  int inc = slice;
-  for (int d = 1; d < tpe; d <<= 1) {
-    const int a = __shfl_up(inc, d, tpe);
-    if (part >= d) inc += a;
-  }
-  const int total = __shfl(inc, tpe - 1, tpe);  // the expert's total
-  if (active && part == 0) tot[e] = total;
-  if (E >= 1024 && tid == 0) {  // (E = 1024: no thread left for row E)
-    const int32_t* rowE = hist + (int64_t)E * B;
-    int nb = 0;
-    for (int b = 0; b < B; b += 16) {
-      int c[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) c[u] = b + u < B ? rowE[b + u] : 0;
+    for (int i = 0; i < RB; ++i) {
+      int t = acc[i];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) nb += c[u];
+      for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+      const int r = r0 + 16 * i;
+      if (lane == 0 && r <= E) tot[r] = t;
     }
-    tot[E] = nb;
   }
   __syncthreads();
-  // exclusive scan of the expert totals 0..E-1 (one per thread), as before
+  // exclusive scan of the expert totals (E <= 1024: one per thread)
   const int mine = tid < E ? tot[tid] : 0;
   int ex = mine;
 #pragma unroll
@@ -230,24 +218,38 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ h
   for (int w2 = 0; w2 < wv; ++w2) base += wsum[w2];
   const int bad = tot[E];
   __syncthreads();
-  if (tid < E) tot[tid] = base + ex - mine;
-  __syncthreads();
-  if (active && e < E) {
-    int run = tot[e] + inc - slice;  // first position of the slice
-    for (int b = b0; b < b1; b += 16) {
-      int c[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) c[u] = b + u < b1 ? row[b + u] : 0;
-#pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (b + u < b1) {
-          row[b + u] = run;
-          run += c[u];
-        }
-    }
-    if (part == 0) offsets[e] = tot[e];
+  if (tid < E) {
+    tot[tid] = base + ex - mine;
+    offsets[tid] = base + ex - mine;
   }
   if (tid == 0) offsets[E] = bad ? -1 : (int32_t)R;
+  __syncthreads();
+  // pass 2: each expert row's exclusive prefix over its blocks, in place
+  for (int r0 = wv; r0 < E; r0 += 16 * RB) {
+    int run[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) run[i] = r0 + 16 * i < E ? tot[r0 + 16 * i] : 0;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      int v[RB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int r = r0 + 16 * i;
+        v[i] = (r < E && b0 + lane < B) ? hist[(int64_t)r * B + b0 + lane] : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        int inc = v[i];
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const int a = __shfl_up(inc, d);
+          if (lane >= d) inc += a;
+        }
+        const int r = r0 + 16 * i;
+        if (r < E && b0 + lane < B) hist[(int64_t)r * B + b0 + lane] = run[i] + inc - v[i];
+        run[i] += __shfl(inc, 63);
+      }
+    }
+  }
 }
 
 __global__ __launch_bounds__(256) void sort_scatter_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
