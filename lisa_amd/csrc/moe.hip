@@ -179,6 +179,94 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ h
   __shared__ int wsum[16];
   __shared__ int tot[1025];  // row totals, then the experts' first positions
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (B <= 16) {
+    // a thread per row (row E: the invalid ids), its <= 16 counts in
+    // registers from one round of loads
+    int v[16], total = 0;
+    const bool act = tid <= E;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = (act && u < B) ? hist[(int64_t)tid * B + u] : 0;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) total += v[u];
+    if (act) tot[tid] = total;
+    if (E >= 1024 && tid == 0) {  // (E = 1024: no thread left for row E)
+      int nb = 0;
+      for (int u = 0; u < B; ++u) nb += hist[(int64_t)E * B + u];
+      tot[E] = nb;
+    }
+    __syncthreads();
+    const int mine = tid < E ? total : 0;
+    int ex = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int a = __shfl_up(ex, d);
+      if (lane >= d) ex += a;
+    }
+    if (lane == 63) wsum[wv] = ex;
+    __syncthreads();
+    int base = 0;
+    for (int w2 = 0; w2 < wv; ++w2) base += wsum[w2];
+    if (tid < E) {
+      int run = base + ex - mine;
+      offsets[tid] = run;
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < B) {
+          hist[(int64_t)tid * B + u] = run;
+          run += v[u];
+        }
+    }
+    if (tid == 0) offsets[E] = tot[E] ? -1 : (int32_t)R;
+    return;
+  }
+  if (E < 256 && B <= 64) {
+    // one batch: all rows' counts in registers from one round of loads
+    // (rows wv + 16 i, i < 16), nothing read twice
+    int v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = wv + 16 * i;
+      v[i] = (r <= E && lane < B) ? hist[(int64_t)r * B + lane] : 0;
+    }
+    int inc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      inc[i] = v[i];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int a = __shfl_up(inc[i], d);
+        if (lane >= d) inc[i] += a;
+      }
+      const int r = wv + 16 * i;
+      if (lane == 63 && r <= E) tot[r] = inc[i];
+    }
+    __syncthreads();
+    const int mine = tid < E ? tot[tid] : 0;
+    int ex = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int a = __shfl_up(ex, d);
+      if (lane >= d) ex += a;
+    }
+    if (lane == 63) wsum[wv] = ex;
+    __syncthreads();
+    int base = 0;
+    for (int w2 = 0; w2 < wv; ++w2) base += wsum[w2];
+    const int bad = tot[E];
+    __syncthreads();
+    if (tid < E) {
+      tot[tid] = base + ex - mine;
+      offsets[tid] = base + ex - mine;
+    }
+    if (tid == 0) offsets[E] = bad ? -1 : (int32_t)R;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = wv + 16 * i;
+      if (r < E && lane < B) hist[(int64_t)r * B + lane] = tot[r] + inc[i] - v[i];
+    }
+    return;
+  }
   // pass 1: row totals
   for (int r0 = wv; r0 <= E; r0 += 16 * RB) {
     int acc[RB];
