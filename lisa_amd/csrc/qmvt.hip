@@ -531,7 +531,10 @@ QmvConfig qmvt_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool al
   c.tiles = (int)((N + 15) / 16);
   c.NW = 4;
   if (c.tiles * 4 < 2048 && nws >= 16) c.NW = 8;
-  c.NW = tune_int("LISAQ_QMVT_NW", c.NW) == 8 ? 8 : 4;
+  {
+    const int v = tune_int("LISAQ_QMVT_NW", c.NW);  // (tuning builds: 1, 2, 4 or 8)
+    if (v == 1 || v == 2 || v == 4 || v == 8) c.NW = v;
+  }
   // x slab: at most ~40 KB of staged x, a whole number of W slabs
   const int64_t per_group = (int64_t)gs * M * 2;
   int SG = G;
