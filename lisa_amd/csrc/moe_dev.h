@@ -6,9 +6,18 @@
 namespace lisaq {
 
 // silu of a bf16 value in bf16 arithmetic: sigmoid rounded to bf16, then the
-// product rounded (exact_header.metal:2-6, mlx_silu on T = bfloat16)
+// product rounded (exact_header.metal:2-6, mlx_silu on T = bfloat16).
+// e^|g| = 2^(|g| log2 e) on the hardware exp2 and 1 / (1 + e) on the hardware
+// reciprocal: each within about 1 ulp of f32 (the product |g| log2 e adds at
+// most |g| 2^-24 to the exponent, ~2^-18 relative at |g| = 88), far finer
+// than the bf16 rounding of the sigmoid that follows, so the result matches a
+// correctly rounded sigmoid except for values within ~2^-10 of a bf16 ulp of a
+// rounding boundary.  (A libm-style exp and an IEEE divide took ~35 VALU
+// operations per element: the gate|up matmul's epilogue computes 64 per
+// thread.)
 __device__ __forceinline__ float silu_bf16(float g) {
-  const float y = 1.0f / (1.0f + expf(fabsf(g)));
+  const float e = __builtin_amdgcn_exp2f(fabsf(g) * 1.44269504088896341f);
+  const float y = __builtin_amdgcn_rcpf(1.0f + e);
   const float sg = bf2f(f2bf(g < 0.0f ? y : 1.0f - y));
   return bf2f(f2bf(__fmul_rn(g, sg)));
 }

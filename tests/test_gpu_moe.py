@@ -191,7 +191,8 @@ def test_moe_forward_parity(dev, oracle, T):
                                                     (64, 128, 8, 2048, 768, 4, 64, True),
                                                     (200, 128, 8, 2048, 768, 4, 64, True),
                                                     (40, 16, 2, 512, 320, 2, 64, True),
-                                                    (9, 8, 3, 256, 256, 4, 128, False)])
+                                                    (9, 8, 3, 256, 256, 4, 128, False),
+                                                    (24, 16, 4, 256, 192, 4, 32, True)])
 def test_moe_forward_gate_up_matvec(dev, monkeypatch, T, E, k, H, I, bits, gs, skew):
     """Between the decode window and the gate|up matmul path (9 <= T, T*k < 20E): gate|up + SwiGLU in
     the gate|up streaming matvec (and the gate|up matmul for runs at or above the matvec limit; skewed
