@@ -969,8 +969,14 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   }
   if ((rc = lisaq_moe_route(st, logits, T, E, k, idx, wts))) return rc;
   LISAQ_REQUIRE(E <= 1024, LISAQ_EINVAL_SHAPE, "moe_forward: need E <= 1024 (E=%d)", E);
-  if ((rc = launch_sort_parallel(st, idx, R, E, k, sorted, order, rows, inv, offs, (int32_t*)(B + L.hist))))
+  // few ids: the one-workgroup sort (one launch instead of three; the same
+  // permutation and offsets; measured at E = 128, k = 8: T = 16 78 -> 75 us,
+  // T = 64 124 -> 120 us, no gain from T = 256)
+  if (R <= tune_int("LISAQ_SORT1_MAX", 1024)) {
+    if ((rc = launch_sort(st, idx, R, E, k, sorted, order, rows, inv, offs))) return rc;
+  } else if ((rc = launch_sort_parallel(st, idx, R, E, k, sorted, order, rows, inv, offs, (int32_t*)(B + L.hist)))) {
     return rc;
+  }
   if (moe_gu_path(T, H, I, E, k, gs, bits)) {
     // gate|up + SwiGLU in one matmul launch reading x through the row map,
     // then the down gather and the combine

@@ -296,14 +296,15 @@ def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
     assert_close_bf16(outs["1"][0], bf16_bits_to_f32(outs["0"][0]), what=f"fused vs generic T={T} k={k} bits={bits}")
 
 
-@pytest.mark.parametrize("T,E,k,H,I", [(600, 64, 8, 128, 64), (40, 1024, 4, 256, 128), (50, 1023, 2, 256, 128)])
+@pytest.mark.parametrize("T,E,k,H,I", [(600, 64, 8, 128, 64), (300, 1024, 4, 256, 128), (600, 1023, 2, 256, 128),
+                                       (2100, 1024, 4, 256, 128)])
 def test_moe_forward_generic_equals_composition(dev, monkeypatch, T, E, k, H, I):
     """moe_forward's generic path (multi-workgroup counting sort, tile tables
     built from the expert offsets) against the same steps composed from the
     public entry points (one-workgroup sort, tile tables from the sorted ids):
     bit-identical, at a size where the sort spans several workgroups
     (T=600, k=8: 4800 ids), and at E = 1024 / 1023 experts (the sort's scan
-    with one thread per expert row)."""
+    with one thread per expert row, and with a wave per row at 17 blocks)."""
     import torch
 
     monkeypatch.setenv("LISAQ_MOE_FUSED", "0")
