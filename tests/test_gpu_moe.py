@@ -62,6 +62,19 @@ def test_combine_bit_exact(dev, oracle, T, k, H):
     assert np.array_equal(got, oracle.moe_combine(down, w, inv, T, k))
 
 
+def test_combine_known_answer(dev):
+    """The combine's association on the GPU (the case of the oracle's known-answer test, H = 8 for the
+    vector kernel and H = 3 for the scalar one): slots 8 and 9 fold into partials 0 and 1, so
+    2^24 - 2^24 + 1 + 1 over ten slots gives 1.0, not the slot-order 2.0."""
+    k = 10
+    for H in (8, 3):
+        vals = np.zeros((k, H), np.float32)
+        vals[0, :], vals[1, :], vals[8, :], vals[9, :] = 2.0**24, -(2.0**24), 1.0, 1.0
+        got = ops.moe_combine(to_dev_bf16(f32_to_bf16_bits(vals), dev), to_dev(np.ones(k, np.float32), dev),
+                              to_dev(np.arange(k, dtype=np.int32), dev), 1, k)
+        assert np.array_equal(bf16_bits_to_f32(from_dev_bf16(got)), np.ones((1, H), np.float32)), H
+
+
 def _expert_stack(rng, E, N, K, bits=4):
     ws, ss, bs = [], [], []
     for _ in range(E):

@@ -237,6 +237,24 @@ def test_moe_combine_chain_order(oracle, k):
     assert np.array_equal(got, f32_to_bf16_bits(ref))
 
 
+def test_moe_combine_known_answer(oracle):
+    """colsum_small<K> (exact_header.metal:12-24) by hand, k = 10 (8 partial sums; slots 8 and 9 join
+    partials 0 and 1), weights 1: products p0 = 2^24, p1 = -2^24, p8 = p9 = 1, the rest 0.
+    t0 = p8 + (p0 + 0) = 1 + 2^24 -> 2^24 (f32 tie to even); t1 = p9 + (p1 + 0) = -16777215 (exact);
+    total = t1 + t0 = 1, then + 0 six times: 1.0.  Summing the slots in order gives 2.0, summing the
+    partials the other way round also 1.0 but t0 first absorbing p8 is what loses the 1."""
+    k, T, H = 10, 1, 2
+    vals = np.zeros((k, H), np.float32)
+    vals[0, 0], vals[1, 0], vals[8, 0], vals[9, 0] = 2.0**24, -(2.0**24), 1.0, 1.0
+    vals[:, 1] = 0.5  # ten halves: 5.0 in any order
+    down = f32_to_bf16_bits(vals)
+    w = np.ones(k, np.float32)
+    inv = np.arange(k, dtype=np.int32)
+    got = bf16_bits_to_f32(oracle.moe_combine(down, w, inv, T, k))
+    assert got.tolist() == [[1.0, 5.0]]
+    assert float(np.float32(sum(np.float32(v) for v in vals[:, 0]))) == 2.0  # the slot-order sum differs
+
+
 def test_qmv_threads_matches_single(oracle):
     rng = np.random.default_rng(6)
     N, K = 300, 512
