@@ -195,16 +195,16 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   const int64_t mr = (max_run > 0 && max_run < R) ? max_run : R;
   L.Mmax = (int)((mr < L.limit - 1) ? mr : L.limit - 1);
   if (L.Mmax < 1) L.Mmax = 1;
+  const int64_t avg = R / (runs > 0 ? runs : 1);  // average run length
   int mv = tune_int("LISAQ_GATHER_MV_ROWS", kGatherMvRows);
   if (mv < 1) mv = 1;
   // runs averaging at least half the limit leave few runs to the matvec: one
   // class (one launch) then, sized for the limit (a row's arithmetic does not
   // depend on the class it runs in; measured at E = 128, k = 8: T = 512 213 ->
   // 210 us, T = 4096 569 -> 561 us)
-  if (2 * (R / (runs > 0 ? runs : 1)) >= L.limit) mv = L.Mmax;
+  if (2 * avg >= L.limit) mv = L.Mmax;
   L.mv[0].M = L.Mmax < mv ? L.Mmax : mv;
   L.mv[1].M = L.Mmax > mv ? L.Mmax : 0;
-  const int64_t avg = R / (runs > 0 ? runs : 1);  // average run length
   size_t o = 256;
   for (int j = 0; j < 2; ++j) {
     GatherMv& c = L.mv[j];
