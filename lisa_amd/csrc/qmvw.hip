@@ -60,7 +60,7 @@ __device__ __forceinline__ uint32_t ror8(uint32_t v) {
 
 }  // namespace
 
-template <int MP, int NW, int GS, int RING>
+template <int MP, int NW, int GS, int RING, int NP>
 __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
   static_assert(MP == 1 || MP == 2 || MP == 4 || MP == 8, "rows of x");
   static_assert(GS == 64 || GS == 128, "group size");
@@ -76,13 +76,48 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
   const int r0 = (int)((int64_t)N * blockIdx.x / p.S);
   const int r1 = (int)((int64_t)N * (blockIdx.x + 1) / p.S);
   const int rows = r1 - r0;
-  const int units = ((rows + 15) >> 4) * segs;
+  const int T = (rows + 15) >> 4;  // 16-row tiles of the block
   const uint32_t rowbytes = (uint32_t)K / 2;
+  // x staged in p.S_inner passes over K (1, or 2 where all of K does not fit
+  // the LDS): pass ps holds segments [ps * segp, ...); the units of a pass
+  // are padded to a multiple of NW so that every wave reaches the barrier
+  // between passes at the same iteration.  A unit's arithmetic does not
+  // depend on the pass count.
+  constexpr int npass = NP;
+  const int segp = (segs + npass - 1) / npass;        // segments per pass
+  const int U0 = T * (segs < segp ? segs : segp);     // units of pass 0
+  const int U0p = (U0 + NW - 1) / NW * NW;            // (padded)
+  const int U1 = T * segs - U0;                       // units of pass 1 (0 if one pass)
+  const int kswitch = U0p / NW;                       // a wave's first iteration of pass 1
+  const int kiters = kswitch + (U1 + NW - 1) / NW;    // iterations of every wave
+  // unit of iteration k of this wave: tile t, segment g (-1: padding)
+  auto unit_of = [&](int k, int& t, int& g) {
+    const int u = wave + k * NW;
+    if constexpr (NP == 1) {
+      if (u >= U0) return false;
+      t = u / segs;
+      g = u - t * segs;
+      return true;
+    }
+    if (u < U0p) {
+      if (u >= U0) return false;
+      const int sp = segs < segp ? segs : segp;
+      t = u / sp;
+      g = u - t * sp;
+      return true;
+    }
+    const int l = u - U0p, sp = segs - segp;
+    if (l >= U1) return false;
+    t = l / sp;
+    g = segp + (l - t * sp);
+    return true;
+  };
+  const int KP = segp * 512;  // columns of x staged per pass
   // staged row m of x at m * XS + 16 * sig(m): the 16-byte slots (mod 256
   // bytes) that one step's A reads hit are sig(m) + 4 q for the lane groups
   // q = 0, 1 (2, 3) reading rows m < 8 -- all distinct with sig(m) = (m & 3)
   // + 8 (m >> 2), so a half-wave's reads take no bank conflicts
-  const int XS = 2 * K + 256;
+  const int XS = 2 * KP + 256;
   auto xrow = [&](int m) { return m * XS + 16 * ((m & 3) + 8 * (m >> 2)); };
   unsigned char* ximg = smem;
   float* sxt = reinterpret_cast<float*>(smem + MP * XS);  // [K/64][MP] block sums of x
@@ -101,9 +136,8 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
   const uint32_t w_lane0 = (uint32_t)(n16 & 7) * rowbytes + (uint32_t)(n16 >> 3) * 64 + q * 16;
   const uint32_t w_lane1 = (uint32_t)(8 + (n16 & 7)) * rowbytes + (uint32_t)(1 - (n16 >> 3)) * 64 + q * 16;
   auto issue = [&](int slot, int k) {
-    const int u = wave + k * NW;
-    const bool ok = u < units;
-    const int t = ok ? u / segs : 0, g = ok ? u - t * segs : 0;
+    int t = 0, g = 0;
+    const bool ok = unit_of(k, t, g);
     const uint32_t tb = (uint32_t)t * 16 * rowbytes + (uint32_t)g * 256;
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
@@ -128,13 +162,15 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
 #pragma unroll
   for (int d = 0; d < RING - 1; ++d) issue(d, d);
 
-  // --- x into LDS, each 8 codes in unpack order (x0,x4,x1,x5,x2,x6,x3,x7)
-  {
-    const int nblk = MP * (K / 8);  // 16-byte blocks; rows m >= M read as zero
+  // --- x of pass ps into LDS, each 8 codes in unpack order (x0,x4,x1,x5,x2,x6,x3,x7),
+  // then the block sums of x (64 codes; a fixed order per (row, block))
+  auto stage = [&](int ps) {
+    const int c0 = ps * KP, kc = (K - c0 < KP ? K - c0 : KP);  // columns of this pass
+    const int nblk = MP * (kc / 8);  // 16-byte blocks; rows m >= M read as zero
     for (int i = tid; i < nblk; i += 64 * NW) {
-      const int m = i / (K / 8), c = i - m * (K / 8);
+      const int m = i / (kc / 8), c = i - m * (kc / 8);
       const u32x4 v = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(m * K + c * 8) * 2, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(m * K + c0 + c * 8) * 2, 0, 0));
       u32x4 o;
       o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);  // (x0, x4)
       o[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);  // (x1, x5)
@@ -142,24 +178,24 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
       o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);  // (x3, x7)
       *reinterpret_cast<u32x4*>(ximg + xrow(m) + c * 16) = o;
     }
-  }
-  __syncthreads();
-  // block sums of x (64 codes), a fixed order per (row, block)
-  for (int i = tid; i < MP * (K / 64); i += 64 * NW) {
-    const int blk = i / MP, m = i - blk * MP;
-    const u32x4* src = reinterpret_cast<const u32x4*>(ximg + xrow(m) + blk * 128);
-    float a0 = 0.f, a1 = 0.f;
+    __syncthreads();
+    for (int i = tid; i < MP * (kc / 64); i += 64 * NW) {
+      const int blk = i / MP, m = i - blk * MP;
+      const u32x4* src = reinterpret_cast<const u32x4*>(ximg + xrow(m) + blk * 128);
+      float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const u32x4 v = src[j];
-      a0 = qmvdev::pdot2(v[0], 0x3F803F80u, a0);
-      a1 = qmvdev::pdot2(v[1], 0x3F803F80u, a1);
-      a0 = qmvdev::pdot2(v[2], 0x3F803F80u, a0);
-      a1 = qmvdev::pdot2(v[3], 0x3F803F80u, a1);
+      for (int j = 0; j < 8; ++j) {
+        const u32x4 v = src[j];
+        a0 = qmvdev::pdot2(v[0], 0x3F803F80u, a0);
+        a1 = qmvdev::pdot2(v[1], 0x3F803F80u, a1);
+        a0 = qmvdev::pdot2(v[2], 0x3F803F80u, a0);
+        a1 = qmvdev::pdot2(v[3], 0x3F803F80u, a1);
+      }
+      sxt[(c0 / 64 + blk) * MP + m] = a0 + a1;
     }
-    sxt[blk * MP + m] = a0 + a1;
-  }
-  __syncthreads();
+    __syncthreads();
+  };
+  stage(0);
 
   // --- this lane's roles
   const int am = n16 & 7, ah = n16 >> 3;                   // A operand: x row, half
@@ -180,14 +216,15 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
     for (int i = 0; i < 4; ++i) av[st][i] = u32x4{0u, 0u, 0u, 0u};
 
   auto compute = [&](int slot, int k) {
-    const int u = wave + k * NW;
-    const int g = u % segs;
+    int t = 0, g = 0;
+    if (!unit_of(k, t, g)) return;  // (padding of pass 0; wave-uniform)
+    const int gl = g - (g >= segp ? segp : 0);  // segment within the staged pass
     if (a_on) {
 #pragma unroll
       for (int st = 0; st < 4; ++st)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          av[st][i] = *reinterpret_cast<const u32x4*>(abase + (4 * g + st) * 256 + i * 16);
+          av[st][i] = *reinterpret_cast<const u32x4*>(abase + (4 * gl + st) * 256 + i * 16);
     }
     f32x4w D[4];
 #pragma unroll
@@ -231,24 +268,32 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
 #pragma unroll
       for (int r = 0; r < RP; ++r) acc[r] = fmaf(sc, D[st][r], fmaf(c, sxp[r], acc[r]));
     }
-    float* dst = part + ((int64_t)u * 64 + lane) * RP;
+    float* dst = part + ((int64_t)(t * segs + g) * 64 + lane) * RP;
 #pragma unroll
     for (int r = 0; r < RP; ++r) dst[r] = acc[r];
   };
 
-  const int cnt = wave < units ? (units - 1 - wave) / NW + 1 : 0;
+  // two passes: every wave runs the same number of iterations (kiters), so
+  // that the barrier between the passes is reached by all of them at
+  // iteration kswitch; one pass: each wave its own units
+  const int cnt = NP == 1 ? (wave < U0 ? (U0 - 1 - wave) / NW + 1 : 0) : kiters;
   for (int k0 = 0; k0 < cnt; k0 += RING) {
 #pragma unroll
     for (int d = 0; d < RING; ++d) {
       issue((d + RING - 1) % RING, k0 + d + RING - 1);
-      if (k0 + d < cnt) compute(d, k0 + d);
+      if (k0 + d < cnt) {
+        if (NP > 1 && k0 + d == kswitch) {
+          __syncthreads();  // (every read of pass 0's x done)
+          stage(1);
+        }
+        compute(d, k0 + d);
+      }
     }
   }
   __syncthreads();
 
   // --- y = sum over segments (in order) of the two halves, one bf16 rounding
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y, (uint32_t)M * N * 2);
-  const int T = (rows + 15) >> 4;
   for (int i = tid; i < T * 16 * M; i += 64 * NW) {
     const int m = i % M, rest = i / M;
     const int n = rest & 15, t = rest >> 4;
@@ -268,9 +313,10 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
 // ---------------------------------------------------------------------------
 // host side
 
-static int qmvw_lds(int MP, int64_t K, int T) {
+static int qmvw_lds(int MP, int64_t K, int T, int passes) {
   const int RP = MP < 4 ? MP : 4;
-  return (int)(MP * (2 * K + 256) + (K / 64) * MP * 4 + (int64_t)T * (K / 512) * 64 * RP * 4);
+  const int64_t segs = K / 512, KP = (segs + passes - 1) / passes * 512;  // x columns staged per pass
+  return (int)(MP * (2 * KP + 256) + (K / 64) * MP * 4 + (int64_t)T * segs * 64 * RP * 4);
 }
 
 QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
@@ -287,7 +333,13 @@ QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   if (P < 1 || (NW != 4 && NW != 8) || ring < 2 || ring > 4) return c;
   if (P > N) P = (int)N;
   const int T = (int)(((N + P - 1) / P + 15) / 16);
-  const int lds = qmvw_lds(MP, K, T);
+  // x staged in one pass over K, or two where one does not fit (eight rows at
+  // K = 9728)
+  int passes = 1, lds = qmvw_lds(MP, K, T, 1);
+  if (lds > 160 * 1024 && K / 512 >= 2 && MP == 8) {
+    passes = 2;
+    lds = qmvw_lds(MP, K, T, 2);
+  }
   if (lds > 160 * 1024) return c;
   c.MR = MP;
   c.NW = NW;
@@ -295,6 +347,7 @@ QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   c.tiles = P;  // grid
   c.U = ring;  // ring depth (units)
   c.tile_rows = T;
+  c.S_inner = passes;
   c.lds_bytes = lds;
   c.ws_bytes = 0;
   c.kind = 5;
@@ -309,19 +362,20 @@ typedef void (*qmvw_fn)(QmvParams);
 
 template <int MP, int GS>
 static qmvw_fn qmvw_pick_nw(int nw, int ring) {
-  if (nw == 8 && ring == 2) return qmvw_kernel<MP, 8, GS, 2>;
+  if (nw == 8 && ring == 2) return qmvw_kernel<MP, 8, GS, 2, 1>;
 #ifdef LISAQ_TUNING
-  if (nw == 4 && ring == 2) return qmvw_kernel<MP, 4, GS, 2>;
-  if (nw == 4 && ring == 3) return qmvw_kernel<MP, 4, GS, 3>;
-  if (nw == 4 && ring == 4) return qmvw_kernel<MP, 4, GS, 4>;
-  if (nw == 8 && ring == 3) return qmvw_kernel<MP, 8, GS, 3>;
-  if (nw == 8 && ring == 4) return qmvw_kernel<MP, 8, GS, 4>;
+  if (nw == 4 && ring == 2) return qmvw_kernel<MP, 4, GS, 2, 1>;
+  if (nw == 4 && ring == 3) return qmvw_kernel<MP, 4, GS, 3, 1>;
+  if (nw == 4 && ring == 4) return qmvw_kernel<MP, 4, GS, 4, 1>;
+  if (nw == 8 && ring == 3) return qmvw_kernel<MP, 8, GS, 3, 1>;
+  if (nw == 8 && ring == 4) return qmvw_kernel<MP, 8, GS, 4, 1>;
 #endif
   return nullptr;
 }
 
 template <int GS>
-static qmvw_fn qmvw_pick(int mp, int nw, int ring) {
+static qmvw_fn qmvw_pick(int mp, int nw, int ring, int passes) {
+  if (passes == 2) return (mp == 8 && nw == 8 && ring == 2) ? qmvw_kernel<8, 8, GS, 2, 2> : nullptr;
   if (mp == 1) return qmvw_pick_nw<1, GS>(nw, ring);
   if (mp == 2) return qmvw_pick_nw<2, GS>(nw, ring);
   if (mp == 4) return qmvw_pick_nw<4, GS>(nw, ring);
@@ -331,13 +385,14 @@ static qmvw_fn qmvw_pick(int mp, int nw, int ring) {
 
 int qmvw_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
   qmvw_fn fn = nullptr;
-  if (bits == 4 && gs == 64) fn = qmvw_pick<64>(c.MR, c.NW, c.U);
-  else if (bits == 4 && gs == 128) fn = qmvw_pick<128>(c.MR, c.NW, c.U);
+  if (bits == 4 && gs == 64) fn = qmvw_pick<64>(c.MR, c.NW, c.U, c.S_inner);
+  else if (bits == 4 && gs == 128) fn = qmvw_pick<128>(c.MR, c.NW, c.U, c.S_inner);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmvw: bits=%d gs=%d rows=%d", bits, gs, c.MR);
-  if (p.tiles || p.M < 1 || p.M > c.MR || p.K % 512 != 0 || grid_x != c.S ||
-      (int64_t)c.tile_rows * 16 * c.S < p.N || qmvw_lds(c.MR, p.K, c.tile_rows) != c.lds_bytes)
+  if (p.tiles || p.M < 1 || p.M > c.MR || p.K % 512 != 0 || grid_x != c.S || (c.S_inner != 1 && c.S_inner != 2) ||
+      (int64_t)c.tile_rows * 16 * c.S < p.N || qmvw_lds(c.MR, p.K, c.tile_rows, c.S_inner) != c.lds_bytes)
     return set_error(LISAQ_EINVAL_SHAPE, "qmvw: launch does not match its configuration");
   p.S = c.S;
+  p.S_inner = c.S_inner;
   if (int rc = allow_dyn_lds((const void*)fn, c.lds_bytes, "qmvw")) return rc;
   hipLaunchKernelGGL(fn, dim3(grid_x), dim3(64 * c.NW), c.lds_bytes, stream, p);
   return check_launch("qmvw");

@@ -130,11 +130,12 @@ def test_qmv_addnorm_rejections():
 
 def test_workspace_queries():
     lib = _lib.load()
-    # one row: no workspace; a few rows over few row tiles (N = 2560: 160 tiles of 16 rows; eight rows
-    # of x staged at K = 9728 exceed the one-stream kernel's LDS): the streaming matvec splits K in four,
-    # f32 parts [4][8][2560]
+    # one row: no workspace; 2-8 rows: the one-stream kernel (eight rows at K = 9728 stage x in two
+    # passes), no workspace; 9 rows over few row tiles (N = 2560: 160 tiles of 16 rows): the streaming
+    # matvec splits K in four, f32 parts [4][9][2560]
     assert lib.lisaq_quantized_matmul_workspace(1, 17408, 5120, 64, 4) == 0
-    assert lib.lisaq_quantized_matmul_workspace(8, 2560, 9728, 64, 4) == 4 * 8 * 2560 * 4
+    assert lib.lisaq_quantized_matmul_workspace(8, 2560, 9728, 64, 4) == 0
+    assert lib.lisaq_quantized_matmul_workspace(9, 2560, 9728, 64, 4) == 4 * 9 * 2560 * 4
     assert lib.lisaq_quantized_matmul_workspace(4, 2560, 9728, 64, 4) == 0  # one-stream kernel
     assert lib.lisaq_quantized_matmul_workspace(8, 17408, 5120, 64, 4) == 0
     # matmul at M=2048, N=17408: 68 x 8 = 544 tiles of 256 x 256; the 32 past two full rounds of 256 CUs are
