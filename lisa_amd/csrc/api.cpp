@@ -153,7 +153,7 @@ static int run_qmm(hipStream_t st, const void* x, const uint32_t* w, const void*
 }
 
 // Gather workspace layout: [counts 256 B][matvec table 0][matvec table 1]
-// [qmm table], 256-B aligned.  Matvec class 0 takes the runs of at most mv[0].M
+// [qmm table][short qmm table], 256-B aligned.  Matvec class 0 takes the runs of at most mv[0].M
 // rows (a kernel sized for them stages all of K at once), class 1 (present when
 // runs of mv[0].M < len < limit can occur) the longer ones.
 struct GatherMv {
@@ -167,9 +167,11 @@ struct GatherLayout {
   bool gu;     // gate|up tables: a matvec entry covers the same rows of both
   bool gu_ok;  // (gu) the matvec classes run the gate|up streaming kernel
   int limit, Mmax, qmm_cap;
+  int qs_cap;  // short tiles (kShortBM rows): the last tile of a run when it holds at most that many rows
   GatherMv mv[2];
-  size_t qmm_off, total;
+  size_t qmm_off, qs_off, total;
   QmmConfig mc;
+  bool mm() const { return qmm_cap > 0 || qs_cap > 0; }  // any matmul tiles
 };
 
 static size_t up256(size_t v) { return (v + 255) / 256 * 256; }
@@ -252,9 +254,18 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
     L.mc.BM = qmm_gu_rows(R, E);
     L.mc.BN = kGuBN;
   }
-  L.qmm_cap = (mr >= L.limit) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ((N + L.mc.BN - 1) / L.mc.BN)) : 0;
+  // A run's last tile of at most kShortBM rows goes to a kernel of short
+  // tiles (two workgroups per CU): in the tall kernel it costs about half a
+  // full tile (its copies and dequantization are those of a full one).  When
+  // no run can be longer than that, the tall launch is left out.
+  const bool mm = mr >= L.limit;
+  const bool short_ok = mm && L.mc.BM > kShortBM && path_int("LISAQ_GATHER_SHORT", 1) != 0;
+  const int64_t ntbn = (N + L.mc.BN - 1) / L.mc.BN;
+  L.qmm_cap = (mm && !(short_ok && mr <= kShortBM)) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ntbn) : 0;
+  L.qs_cap = short_ok ? (int)(runs * ntbn) : 0;
   L.qmm_off = o;
-  L.total = L.qmm_off + up256((size_t)L.qmm_cap * 16);
+  L.qs_off = L.qmm_off + up256((size_t)L.qmm_cap * 16);
+  L.total = L.qs_off + up256((size_t)L.qs_cap * 16);
   return L;
 }
 
@@ -275,6 +286,9 @@ static TileTableJob gather_job(const GatherLayout& L, int64_t N, void* ws) {
   }
   j.qmm_tab = (int4*)(base + L.qmm_off);
   j.qmm_cap = L.qmm_cap;
+  j.SBM = kShortBM;
+  j.qs_tab = L.qs_cap ? (int4*)(base + L.qs_off) : nullptr;
+  j.qs_cap = L.qs_cap;
   j.counts = (int32_t*)base;
   return j;
 }
@@ -310,7 +324,7 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
     rc = qmv_launch(st, c.qc, p, bits, gs, c.grid);
     if (rc) return rc;
   }
-  if (L.qmm_cap > 0) {
+  if (L.mm()) {
     QmmParams p{};
     p.x = (const uint16_t*)x;
     p.w = w;
@@ -322,8 +336,15 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
     p.N = (int)N;
     p.K = (int)K;
     p.G = (int)(K / gs);
-    rc = L.mc.MT == 8 ? qmm_gather_tall_launch(st, p, bits, gs, L.qmm_cap) : qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
-    if (rc) return rc;
+    if (L.qmm_cap > 0) {
+      rc = L.mc.MT == 8 ? qmm_gather_skip_launch(st, p, bits, gs, L.qmm_cap, 256)
+                        : qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
+      if (rc) return rc;
+    }
+    if (L.qs_cap > 0) {
+      p.tiles = (const int4*)(base + L.qs_off);
+      if ((rc = qmm_gather_skip_launch(st, p, bits, gs, L.qs_cap, kShortBM))) return rc;
+    }
   }
   return LISAQ_OK;
 }
@@ -361,7 +382,7 @@ static int gather_launch_gu(hipStream_t st, const GatherLayout& L, const void* x
     p.tile_stride = c.grid < c.cap ? c.grid : 0;
     if ((rc = qmv_launch(st, c.qc, p, bits, gs, c.grid))) return rc;
   }
-  if (L.qmm_cap > 0) {
+  if (L.mm()) {
     QmmParams p{};
     p.x = (const uint16_t*)x;
     p.w = gw;
@@ -379,7 +400,11 @@ static int gather_launch_gu(hipStream_t st, const GatherLayout& L, const void* x
     p.K = (int)H;
     p.G = (int)(H / gs);
     p.ksplit = 1;
-    if ((rc = qmm_gu_launch(st, p, bits, gs, L.qmm_cap, L.mc.BM))) return rc;
+    if (L.qmm_cap > 0 && (rc = qmm_gu_launch(st, p, bits, gs, L.qmm_cap, L.mc.BM))) return rc;
+    if (L.qs_cap > 0) {
+      p.tiles = (const int4*)(base + L.qs_off);
+      if ((rc = qmm_gu_launch(st, p, bits, gs, L.qs_cap, kShortBM))) return rc;
+    }
   }
   return LISAQ_OK;
 }
@@ -732,11 +757,22 @@ int lisaq_gather_rows(void* stream, const void* x, const int32_t* rows, void* ou
 
 }  // extern "C"
 
-// gate|up tiles of the MoE prefill: every run in 128-row tiles of 128 columns
+// gate|up tiles of the MoE prefill: every run in tiles of qmm_gu_rows rows
+// and 128 columns, a run's last tile of at most kShortBM rows in the short
+// table (see gather_layout)
 static int64_t gu_cap(int64_t R, int64_t I, int E) {
   const int64_t runs = R < E ? R : E;
   const int BM = qmm_gu_rows(R, E);
   return ((R + BM - 1) / BM + runs) * ((I + kGuBN - 1) / kGuBN);
+}
+static int64_t gu_short_cap(int64_t R, int64_t I, int E) {
+  const int64_t runs = R < E ? R : E;
+  return qmm_gu_rows(R, E) > kShortBM && path_int("LISAQ_GATHER_SHORT", 1) != 0 ? runs * ((I + kGuBN - 1) / kGuBN)
+                                                                               : 0;
+}
+// workspace of the gate|up tables: [counts 256 B][tiles][short tiles]
+static size_t gu_ws_bytes(int64_t R, int64_t I, int E) {
+  return 256 + up256((size_t)gu_cap(R, I, E) * 16) + up256((size_t)gu_short_cap(R, I, E) * 16);
 }
 
 // The fused gate|up matmul serves the prefill when the average expert run is
@@ -762,6 +798,9 @@ static TileTableJob gu_job(int64_t R, int64_t I, int E, void* ws) {
   j.mv_vr[0] = j.mv_vr[1] = 16;
   j.qmm_tab = (int4*)(gb + 256);
   j.qmm_cap = (int)gu_cap(R, I, E);
+  j.SBM = kShortBM;
+  j.qs_cap = (int)gu_short_cap(R, I, E);
+  j.qs_tab = j.qs_cap ? (int4*)(gb + 256 + up256((size_t)j.qmm_cap * 16)) : nullptr;
   j.counts = (int32_t*)gb;
   return j;
 }
@@ -773,9 +812,9 @@ static int gate_up_swiglu(hipStream_t st, const void* x, const int32_t* xrows, i
                           const int32_t* offs, const uint32_t* gw, const void* gsc, const void* gbi,
                           const uint32_t* uw, const void* usc, const void* ubi, void* act, int64_t R, int64_t I,
                           int64_t H, int E, int gs, int bits, void* ws, size_t ws_bytes, bool table_ready = false) {
-  const int64_t cap = gu_cap(R, I, E);
-  LISAQ_REQUIRE(ws != nullptr && 256 + (size_t)cap * 16 <= ws_bytes && aligned(ws, 256), LISAQ_EWORKSPACE,
-                "gate|up: 256-byte aligned workspace of %zu bytes required (got %zu)", 256 + (size_t)cap * 16,
+  const int64_t cap = gu_cap(R, I, E), scap = gu_short_cap(R, I, E);
+  LISAQ_REQUIRE(ws != nullptr && gu_ws_bytes(R, I, E) <= ws_bytes && aligned(ws, 256), LISAQ_EWORKSPACE,
+                "gate|up: 256-byte aligned workspace of %zu bytes required (got %zu)", gu_ws_bytes(R, I, E),
                 ws_bytes);
   LISAQ_REQUIRE(T > 0 && T * H < ((int64_t)1 << 31), LISAQ_EINVAL_SHAPE, "gate|up: x larger than 2^31 elements");
   LISAQ_REQUIRE(aligned(act, 16), LISAQ_EINVAL_LAYOUT, "gate|up: act must be 16-byte aligned");
@@ -801,7 +840,10 @@ static int gate_up_swiglu(hipStream_t st, const void* x, const int32_t* xrows, i
   p.K = (int)H;
   p.G = (int)(H / gs);
   p.ksplit = 1;
-  return qmm_gu_launch(st, p, bits, gs, (int)cap, qmm_gu_rows(R, E));
+  if (int rc = qmm_gu_launch(st, p, bits, gs, (int)cap, qmm_gu_rows(R, E))) return rc;
+  if (scap == 0) return LISAQ_OK;
+  p.tiles = (const int4*)(gb + 256 + up256((size_t)cap * 16));
+  return qmm_gu_launch(st, p, bits, gs, (int)scap, kShortBM);
 }
 
 extern "C" {
@@ -825,7 +867,7 @@ int lisaq_gather_qmm(void* stream, const void* x, const uint32_t* w, const void*
   const GatherLayout L = gather_layout(R, N, K, E, gs, bits);
   LISAQ_REQUIRE(ws != nullptr && ws_bytes >= L.total && aligned(ws, 256), LISAQ_EWORKSPACE,
                 "gather_qmm: 256-byte aligned workspace of %zu bytes required (got %zu)", L.total, ws_bytes);
-  if (L.qmm_cap > 0)
+  if (L.mm())
     LISAQ_REQUIRE(K % 64 == 0, LISAQ_EUNSUPPORTED, "gather_qmm: K=%lld must be a multiple of 64", (long long)K);
   hipStream_t st = (hipStream_t)stream;
   rc = gather_tables(st, L, rhs, R, N, E, ws);
@@ -843,7 +885,7 @@ int lisaq_swiglu(void* stream, const void* gate, const void* up, void* act, int6
 
 size_t lisaq_gather_qmm_swiglu_workspace(int64_t R, int64_t I, int E) {
   if (R <= 0 || I <= 0 || E <= 0) return 256;
-  return 256 + up256((size_t)gu_cap(R, I, E) * 16);
+  return gu_ws_bytes(R, I, E);
 }
 
 int lisaq_gather_qmm_swiglu(void* stream, const void* x, const int32_t* x_rows, const int32_t* rhs_indices,
@@ -915,7 +957,7 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
   const size_t g1b = gather_layout(R, I, H, E, gs, bits, T, false, /*gu=*/true).total;
   const size_t g1 = g1a > g1b ? g1a : g1b;
   const size_t g2 = gather_layout(R, H, I, E, gs, bits, T, moe_down_tall(T, H, I, E, k, gs, bits)).total;
-  const size_t g3 = 256 + up256((size_t)gu_cap(R, I, E) * 16);
+  const size_t g3 = gu_ws_bytes(R, I, E);
   // (the down tables and the gate/up tables side by side: both are built by
   // one launch)
   L.gws = take(up256(g2) + (g1 > g3 ? g1 : g3));
@@ -1001,14 +1043,14 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
     // streaming kernel, the matmul runs in the gate|up matmul kernel (both
     // bitwise equal to gate, up and SwiGLU as three steps), no gathered x
     const GatherLayout GU = gather_layout(R, I, H, E, gs, bits, T, false, /*gu=*/true);
-    const bool mm_ok = GU.qmm_cap == 0 || (H % 64 == 0 && I % 64 == 0 && (bits == 2 || bits == 4) &&
+    const bool mm_ok = !GU.mm() || (H % 64 == 0 && I % 64 == 0 && (bits == 2 || bits == 4) &&
                                            (gs == 32 || gs == 64 || gs == 128));
     if (GU.gu_ok && mm_ok && T * H < ((int64_t)1 << 31) && path_int("LISAQ_MOE_GU_MV", 1) != 0) {
       if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
       if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
       if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, d, R, H, I, 1, gs, bits))) return rc;
       const GatherLayout DN = gather_layout(R, H, I, E, gs, bits, T);
-      if (DN.qmm_cap > 0 && (H % 64 || I % 64))
+      if (DN.mm() && (H % 64 || I % 64))
         return set_error(LISAQ_EUNSUPPORTED, "moe_forward: H, I must be multiples of 64 for the matmul path");
       const size_t gu_at = up256(DN.total);
       void* gws_gu = (char*)gws + gu_at;
@@ -1032,7 +1074,7 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   const size_t gu_at = up256(DN.total);
   void* gws_gu = (char*)gws + gu_at;
   LISAQ_REQUIRE(gu_at + GU.total <= gws_bytes, LISAQ_EWORKSPACE, "moe_forward: gather workspace");
-  if ((GU.qmm_cap > 0 || DN.qmm_cap > 0) && (H % 64 || I % 64))
+  if ((GU.mm() || DN.mm()) && (H % 64 || I % 64))
     return set_error(LISAQ_EUNSUPPORTED, "moe_forward: H, I must be multiples of 64 for the matmul path");
   const TileTableJob jobs[2] = {gather_job(DN, H, gws), gather_job(GU, I, gws_gu)};
   if ((rc = launch_tile_table(st, sorted, offs, R, E, jobs, 2))) return rc;

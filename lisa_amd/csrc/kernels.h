@@ -35,16 +35,19 @@ constexpr int kTileTableMaxExperts = 16384;
 // One set of gather tile tables: N output rows per expert; runs shorter than
 // `limit` as matvec tiles, of mv_vr[0] output rows in table mv_tab[0] when
 // they hold at most MV rows, else of mv_vr[1] rows in mv_tab[1]; the others as
-// BM x BN matmul tiles.  Entries past a matvec table's count are written as
-// {-1,..} for mv_pad[j] entries (its launch grid), the matmul table's up to
-// its capacity.  counts[0..2]: matvec tiles, matmul tiles, overflow/bad-ids
-// flag.
+// BM x BN matmul tiles; with a short table (qs_tab, SBM > 0) the last tile of
+// a run goes there, as an SBM x BN tile, when it holds at most SBM rows.
+// Entries past a matvec table's count are written as {-1,..} for mv_pad[j]
+// entries (its launch grid), the matmul tables' up to their capacity.
+// counts[0..2]: matvec tiles, matmul tiles, overflow/bad-ids flag.
 struct TileTableJob {
-  int N, limit, MV, BM, BN;
+  int N, limit, MV, BM, BN, SBM;
   int4* mv_tab[2];
   int mv_cap[2], mv_pad[2], mv_vr[2];
   int4* qmm_tab;
   int qmm_cap;
+  int4* qs_tab;
+  int qs_cap;
   int32_t* counts;
 };
 // gather tile tables (one workgroup per job, 1 or 2 jobs) from the sorted ids

@@ -566,8 +566,8 @@ int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const i
 // run becomes either matvec tiles (run length < limit: {e, start, len, n tile
 // of VR rows}, in one of two tables by run length, <= MV rows or longer, for
 // matvec kernels sized for each) or matmul tiles ({e, start + i*BM, rows, n
-// tile of BN}),
-// matching the reference's per-run quantized_matmul dispatch.  Unused entries
+// tile of BN}; a last tile of at most SBM rows in the short table, for a
+// kernel of SBM-row tiles), matching the reference's per-run quantized_matmul dispatch.  Unused entries
 // up to each table's capacity are written as {-1,..} so a grid of `capacity`
 // workgroups can be launched without a host round trip.  One workgroup:
 //  1. one coalesced pass marks each run's first and last index per expert
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   extern __shared__ int tt_smem[];
   int* rstart = tt_smem;      // [E] first index of expert e's run
   int* rend = tt_smem + E;    // [E] one past its last index (0: no run)
-  __shared__ int s_tot[3][16], s_bad;
+  __shared__ int s_tot[4][16], s_bad;
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += 1024) rstart[e] = rend[e] = 0;
   if (tid == 0) s_bad = 0;
@@ -626,63 +626,74 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   }
   __syncthreads();
   // per-thread tile counts of its experts: matvec class 0 (runs of at most MV
-  // rows), matvec class 1 (longer runs below the limit), matmul
+  // rows), matvec class 1 (longer runs below the limit), matmul, short matmul
+  // (a run's last tile of at most SBM rows; SBM = 0: none)
+  const int SBM = job.qs_tab ? job.SBM : 0;
   const int nv0 = (N + job.mv_vr[0] - 1) / job.mv_vr[0];
   const int nv1 = (N + job.mv_vr[1] - 1) / job.mv_vr[1];
   const int ntbn = (N + BN - 1) / BN;
   const int chunk = (E + 1023) / 1024;
   const int e0 = tid * chunk, e1 = e0 + chunk < E ? e0 + chunk : E;
-  int c[3] = {0, 0, 0};
+  int c[4] = {0, 0, 0, 0};
   for (int e = e0; e < e1; ++e) {
     const int len = rend[e] - rstart[e];
     if (len <= 0) continue;
-    if (len >= limit) c[2] += (len + BM - 1) / BM * ntbn;
-    else if (len <= MV) c[0] += nv0;
+    if (len >= limit) {
+      const int rem = len % BM;
+      const bool sh = rem > 0 && rem <= SBM;
+      c[2] += (len / BM + (rem > 0 && !sh ? 1 : 0)) * ntbn;
+      c[3] += sh ? ntbn : 0;
+    } else if (len <= MV) c[0] += nv0;
     else c[1] += nv1;
   }
   // inclusive scan of the per-thread counts: within each wave by shuffles,
   // then the 16 wave totals
   const int lane = tid & 63, wv = tid >> 6;
-  int inc[3] = {c[0], c[1], c[2]};
+  int inc[4] = {c[0], c[1], c[2], c[3]};
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const int a = __shfl_up(inc[j], d);
       if (lane >= d) inc[j] += a;
     }
   }
   if (lane == 63) {
 #pragma unroll
-    for (int j = 0; j < 3; ++j) s_tot[j][wv] = inc[j];
+    for (int j = 0; j < 4; ++j) s_tot[j][wv] = inc[j];
   }
   __syncthreads();
-  int before[3] = {0, 0, 0}, tot[3] = {0, 0, 0};
+  int before[4] = {0, 0, 0, 0}, tot[4] = {0, 0, 0, 0};
   for (int w2 = 0; w2 < 16; ++w2)
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < 4; ++j) {
       if (w2 < wv) before[j] += s_tot[j][w2];
       tot[j] += s_tot[j][w2];
     }
   const bool bad = s_bad != 0;
-  const int caps[3] = {job.mv_cap[0], job.mv_cap[1], qmm_cap};
-  if (bad) tot[0] = tot[1] = tot[2] = 0;
+  const int caps[4] = {job.mv_cap[0], job.mv_cap[1], qmm_cap, SBM ? job.qs_cap : 0};
+  if (bad) tot[0] = tot[1] = tot[2] = tot[3] = 0;
   if (tid == 0) {
     counts[0] = tot[0] + tot[1];
-    counts[1] = tot[2];
-    counts[2] = (bad || tot[0] > caps[0] || tot[1] > caps[1] || tot[2] > caps[2]) ? 1 : 0;
+    counts[1] = tot[2] + tot[3];
+    counts[2] = (bad || tot[0] > caps[0] || tot[1] > caps[1] || tot[2] > caps[2] || tot[3] > caps[3]) ? 1 : 0;
   }
   if (!bad) {
-    int o[3];
+    int o[4];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) o[j] = before[j] + inc[j] - c[j];
+    for (int j = 0; j < 4; ++j) o[j] = before[j] + inc[j] - c[j];
     for (int e = e0; e < e1; ++e) {
       const int st = rstart[e], len = rend[e] - st;
       if (len <= 0) continue;
       if (len >= limit) {
-        for (int r0 = 0; r0 < len; r0 += BM)
-          for (int nt = 0; nt < ntbn; ++nt, ++o[2])
-            if (o[2] < qmm_cap) qmm_tab[o[2]] = make_int4(e, st + r0, len - r0 < BM ? len - r0 : BM, nt);
+        for (int r0 = 0; r0 < len; r0 += BM) {
+          const int rows = len - r0 < BM ? len - r0 : BM;
+          const bool sh = rows <= SBM;  // (SBM < BM: only a run's last tile)
+          int4* tab = sh ? job.qs_tab : qmm_tab;
+          int& oq = o[sh ? 3 : 2];
+          for (int nt = 0; nt < ntbn; ++nt, ++oq)
+            if (oq < caps[sh ? 3 : 2]) tab[oq] = make_int4(e, st + r0, rows, nt);
+        }
       } else if (len <= MV) {
         for (int nt = 0; nt < nv0; ++nt, ++o[0])
           if (o[0] < caps[0]) job.mv_tab[0][o[0]] = make_int4(e, st, len, nt);
@@ -701,6 +712,7 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
     for (int t = tot[j] + tid; t < hi; t += 1024) job.mv_tab[j][t] = make_int4(-1, 0, 0, 0);
   }
   for (int t = tot[2] + tid; t < qmm_cap; t += 1024) qmm_tab[t] = make_int4(-1, 0, 0, 0);
+  for (int t = tot[3] + tid; t < caps[3]; t += 1024) job.qs_tab[t] = make_int4(-1, 0, 0, 0);
 }
 
 int launch_tile_table(hipStream_t st, const int32_t* ids, const int32_t* offs, int64_t R, int E,

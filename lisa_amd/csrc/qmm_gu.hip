@@ -46,25 +46,32 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
   LISAQ_REQUIRE((int64_t)p.N * p.K * bits / 8 < ((int64_t)1 << 32), LISAQ_EINVAL_SHAPE,
                 "qmm_gu: one weight matrix larger than 4 GiB");
   LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
-  LISAQ_REQUIRE(rows == 128 || rows == 256, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built", rows);
+  LISAQ_REQUIRE(rows == 64 || rows == 128 || rows == 256, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built",
+                rows);
+  if (rows == 64) return gu_launch<2>(stream, p, bits, gs, grid);
   return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
-// Gather launches with 256-row tiles (the MoE prefill's down projection when
-// runs average >= 192 rows): the plain kernel with the empty 32-row blocks'
-// matrix instructions skipped (the last tile of a run is mostly empty).
-int qmm_gather_tall_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid) {
+// Gather launches whose 32-row blocks past a tile's rows skip their matrix
+// instructions: 256-row tiles (the MoE prefill's down projection when runs
+// average >= 192 rows) and 64-row tiles (the short last tile of a run).
+int qmm_gather_skip_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows) {
   qmm_fn fn = nullptr;
   int lds = 0;
-  auto pick = [&](auto bt) {
-    constexpr int B = decltype(bt)::value;
-    lds = QmmLds<B, 64, 8, 1, 8>::TOTAL;
-    if (gs == 32) fn = qmm_kernel<B, 32, 8, 1, 8, false, false, 3, true>;
-    if (gs == 64) fn = qmm_kernel<B, 64, 8, 1, 8, false, false, 3, true>;
-    if (gs == 128) fn = qmm_kernel<B, 128, 8, 1, 8, false, false, 3, true>;
+  auto pick = [&](auto bt, auto mt) {
+    constexpr int B = decltype(bt)::value, MT = decltype(mt)::value;
+    lds = QmmLds<B, 64, MT, 1, 8>::TOTAL;
+    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, false, 3, true>;
+    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, false, 3, true>;
+    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, false, 3, true>;
   };
-  if (bits == 4) pick(std::integral_constant<int, 4>{});
-  if (bits == 2) pick(std::integral_constant<int, 2>{});
+  LISAQ_REQUIRE(rows == 64 || rows == 256, LISAQ_EUNSUPPORTED, "qmm gather: row tile %d not built", rows);
+  auto pick_mt = [&](auto bt) {
+    if (rows == 256) pick(bt, std::integral_constant<int, 8>{});
+    else pick(bt, std::integral_constant<int, 2>{});
+  };
+  if (bits == 4) pick_mt(std::integral_constant<int, 4>{});
+  if (bits == 2) pick_mt(std::integral_constant<int, 2>{});
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm gather: bits=%d group_size=%d not supported", bits, gs);
   LISAQ_REQUIRE(p.tiles && p.K % 64 == 0, LISAQ_EINVAL_LAYOUT, "qmm gather: tile table and K %% 64 == 0 required");
   LISAQ_REQUIRE((int64_t)p.N * p.K * bits / 8 < ((int64_t)1 << 32) && (int64_t)p.M * p.K < ((int64_t)1 << 31),

@@ -503,7 +503,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   constexpr int NCOPY = XI + WI + SBI;               // copies per wave and step
   constexpr int PPW = BITS == 4 ? 4 : 8;             // dequant pieces per packed word
   constexpr int NPIECE = NT * G::WPL * PPW;          // dequant pieces per step
-  static_assert(NCOPY <= 3 * NMF && NPIECE <= SLOTS, "slot plan");
+  static_assert(NCOPY <= 3 * NMF, "slot plan");  // (short tiles: several dequant pieces per slot)
   int xs = 0, ws1 = 1;  // x stage of step k, W stage of step k+1
   auto step = [&](int kt, uint32_t (*bcur)[16], uint32_t (*bnxt)[16], const WLane& wn, WLane& wnn) {
     const int xs2 = xs == 0 ? NB - 1 : xs - 1;    // (k+NB-1) % NB: x copy of this step

@@ -396,3 +396,40 @@ def test_gather_qmm_swiglu(dev, oracle, monkeypatch, T, E, k, H, I, bits, gs):
     assert long_tok.any()
     assert np.array_equal(from_dev_bf16(out)[long_tok], from_dev_bf16(out0)[long_tok])
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("runs", [(300, 64, 65, 256, 320, 1, 40, 129, 0, 513),
+                                  (200, 33, 100, 64, 128, 190, 16, 255)])
+def test_gather_short_last_tiles(dev, oracle, monkeypatch, runs):
+    """A run's last matmul tile of at most 64 rows goes to the short-tile kernel: gather_qmm and
+    gather_qmm_swiglu bitwise equal to the same calls with every tile in the tall kernel
+    (LISAQ_GATHER_SHORT=0), and gather_qmm's runs against the per-run oracle."""
+    import torch
+
+    rng = np.random.default_rng(sum(runs))
+    E, N, K = len(runs), 256, 512
+    W, S, B = _expert_stack(rng, E, N, K)
+    ids = np.repeat(np.arange(E, dtype=np.int32), runs)
+    R = ids.size
+    x = np_x(rng, R, K)
+    args = (to_dev_bf16(x, dev), to_dev_u32(W, dev), to_dev_bf16(S, dev), to_dev_bf16(B, dev))
+    sid = to_dev(ids, dev)
+    T = 700
+    xt = np_x(rng, T, K)
+    xrows = to_dev(rng.integers(0, T, R).astype(np.int32), dev)
+    U = _expert_stack(rng, E, N, K)
+    gate, up = tuple(args[1:]), (to_dev_u32(U[0], dev), to_dev_bf16(U[1], dev), to_dev_bf16(U[2], dev))
+
+    def both():
+        y = from_dev_bf16(ops.gather_qmm(*args, rhs_indices=sid))
+        a = from_dev_bf16(ops.gather_qmm_swiglu(to_dev_bf16(xt, dev), xrows, gate, up, sid))
+        torch.cuda.synchronize()
+        return y, a
+
+    y, a = both()
+    monkeypatch.setenv("LISAQ_GATHER_SHORT", "0")
+    y0, a0 = both()
+    assert np.array_equal(y, y0)
+    assert np.array_equal(a, a0)
+    ref = _gather_ref(oracle, x, W, S, B, ids, ops.qmv_batch_limit(K, N))
+    assert_close_bf16(y, ref)
