@@ -182,10 +182,14 @@ struct QmmLds {
   static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
   static constexpr int X = BM / 8 * XG;            // x tile
   static constexpr int W = BN * RB;                // packed W tile
-  static constexpr int S = BN * 4;                 // scales: the aligned bf16 pair holding the step's group(s)
-  static constexpr int WSTAGE = W + 2 * S;         // packed W + scales + biases of one step
+  static constexpr int WSTAGE = W;                 // packed W of one step
   static constexpr int W0 = NB * X;                // W ring after the x ring
-  static constexpr int TOTAL = NB * (X + WSTAGE);
+  // scales / biases: 8 consecutive groups of each row (16 bytes) per block,
+  // two blocks (double-buffered), each [scales][biases]
+  static constexpr int SBA = BN * 16;              // one array of one block
+  static constexpr int SBB = 2 * SBA;              // one block
+  static constexpr int SB0 = W0 + NB * WSTAGE;     // the two blocks after the W ring
+  static constexpr int TOTAL = SB0 + 2 * SBB;
 };
 
 // WN waves side by side along N, each all BM rows x 32*NT columns: four
@@ -347,13 +351,17 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     const int lb = BITS == 4 ? (off % L::RB) ^ (w_swz(off / L::RB) << 4) : off % L::RB;
     wvo[i] = (uint32_t)n * rowbytes + (uint32_t)lb;
   }
-  // scales / biases: per row the 4-byte-aligned bf16 pair holding the step's
-  // group(s); 64 rows per instruction (BN/64 instructions per array, spread
-  // over the waves)
+  // scales / biases: blocks of 8 groups (SBK = GS / 8 K-steps), 16 bytes of
+  // each row per block and array, 64 rows per instruction (BN/64 instructions
+  // per array, spread over the waves), one block copied every SBK steps into
+  // the block buffer not being read.  (Per K-step the groups of a row are 2-4
+  // bytes: copied per step they made every lane of a copy touch its own cache
+  // line.)
   constexpr int SI = BN / 64;                  // instructions per array
-  constexpr int SBI = SI * 2 / NWV;            // scale/bias instructions per wave
-  static_assert(SBI >= 1 && SI * 2 % NWV == 0, "scale tile geometry");
-  constexpr int VM_X = XI, VM_W = WI + SBI;    // DMA instructions per wave: x tile, W stage
+  constexpr int SBI = SI * 2 / NWV;            // scale/bias instructions per wave and block
+  constexpr int SBK = GS / 8;                  // K-steps per block
+  static_assert(SBI >= 1 && SI * 2 % NWV == 0 && SBK >= 2, "scale tile geometry");
+  constexpr int VM_X = XI, VM_W = WI;          // DMA instructions per wave and step: x tile, W stage
   // copies i0 <= i < i1 of the x tile (i0, i1 compile-time after inlining)
   auto issue_x = [&](int k, int stage, int i0, int i1) {
     unsigned char* st = smem + stage * L::X;
@@ -378,26 +386,27 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     const int nb = nt0 + (up ? blk - SI / 2 : blk) * 64 + lane;
     sbrow[q] = (uint32_t)(nb < p.N ? nb : p.N - 1) * (uint32_t)p.G;
   }
-  // copy q of the W stage of step k: q < WI packed W, else scale/bias copy q - WI
+  // copy q of the W stage of step k
   auto issue_w_part = [&](int k, int stage, int q) {
     unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
     const int k0 = k * BK;
-    if (q < WI) {
-      if (WLANES == 64 || lane < WLANES) buf_lds16(rw, wvo[q], (uint32_t)k0 * BITS / 8, st + wave * WB + q * 1024);
-      return;
-    }
-    const int g = k0 / GS;
-    const int idx = wave + NWV * (q - WI);  // 0 .. 2*SI-1: s row blocks, then b row blocks
-    const bool is_b = idx >= SI;
-    const int blk = is_b ? idx - SI : idx;
-    // (lanes of this instruction load tile rows blk*64 + lane: the aligned
-    // bf16 pair holding element nb * G + g)
-    buf_lds4(rsb[q - WI], ((sbrow[q - WI] + (uint32_t)g) & ~1u) * 2u, 0u,
-               st + L::W + (is_b ? L::S : 0) + blk * 64 * 4);
+    if (WLANES == 64 || lane < WLANES) buf_lds16(rw, wvo[q], (uint32_t)k0 * BITS / 8, st + wave * WB + q * 1024);
   };
   auto issue_w = [&](int k, int stage) {
 #pragma unroll
-    for (int q = 0; q < WI + SBI; ++q) issue_w_part(k, stage, q);
+    for (int q = 0; q < WI; ++q) issue_w_part(k, stage, q);
+  };
+  // scale/bias block sb (groups 8 sb .. 8 sb + 7 of every row; past a row's
+  // end: the next row's groups or zeros, never used) into block buffer sb % 2
+  auto issue_sb = [&](int sb) {
+    unsigned char* st = smem + L::SB0 + (sb & 1) * L::SBB;
+#pragma unroll
+    for (int q = 0; q < SBI; ++q) {
+      const int idx = wave + NWV * q;  // 0 .. 2*SI-1: s row blocks, then b row blocks
+      const bool is_b = idx >= SI;
+      const int blk = is_b ? idx - SI : idx;
+      buf_lds16(rsb[q], sbrow[q] * 2u, (uint32_t)sb * 16u, st + (is_b ? L::SBA : 0) + blk * 64 * 16);
+    }
   };
 
   // ---- one K-step's W of this lane (LDS stage): packed words, scale, bias
@@ -408,18 +417,15 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   };
   auto read_w = [&](int k, int stage, WLane& o) {
     const unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
-    const int g0 = k * BK / GS;
+    // the lane's group (gs 32: the step's two groups, one per half-wave) and
+    // its block buffer
+    const int g = k * BK / GS + (GS == 32 ? h : 0);
+    const unsigned char* sbb = smem + L::SB0 + ((g >> 3) & 1) * L::SBB + (g & 7) * 2;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int r = (wn * NT + nt) * 32 + col;
-      // half of the staged pair: the lane's group (gs 32: the step's two
-      // groups, pair-aligned since G is even; else the element's parity)
-      const int rn = GU ? r % (BN / 2) : r;
-      const int n = nt0 + rn < p.N ? nt0 + rn : p.N - 1;
-      const int half = GS == 32 ? h : (int)(((int64_t)n * p.G + g0) & 1);
-      const int si = r * 4 + half * 2;
-      o.s[nt] = *reinterpret_cast<const uint16_t*>(st + L::W + si);
-      o.b[nt] = *reinterpret_cast<const uint16_t*>(st + L::W + L::S + si);
+      o.s[nt] = *reinterpret_cast<const uint16_t*>(sbb + r * 16);
+      o.b[nt] = *reinterpret_cast<const uint16_t*>(sbb + L::SBA + r * 16);
       const int hp = BITS == 4 ? h ^ w_swz(r) : h;
       o.w[nt] = *reinterpret_cast<const WV*>(st + r * L::RB + hp * (4 * G::WPL));
     }
@@ -457,6 +463,13 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   const int nk = nk_all - kb < per ? nk_all - kb : per;  // (host: every split has >= 1 step)
   auto kc = [&](int k) { return kb + (k < nk ? k : nk - 1); };
   uint32_t bA[NT][16], bB[NT][16];  // B operands of the current / next step
+  // scale/bias blocks: the first two in the prologue; block sb + 1 during
+  // step sb * SBK - 1 (global steps), after the last read of block sb - 1
+  // (step sb * SBK - 3) and landed before the first read of block sb + 1
+  // (step (sb + 1) * SBK - 2); none past the last step's block
+  const int sb_last = (kb + nk - 1) / SBK;
+  issue_sb(kb / SBK);
+  if (kb / SBK + 1 <= sb_last) issue_sb(kb / SBK + 1);
   issue_x(kc(0), 0, 0, XI);
   issue_w(kc(0), 0);
   issue_w(kc(1), 1);
@@ -500,7 +513,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   //    step's LDS reads, then the workgroup barrier.
   constexpr int NMF = MT * NT;
   constexpr int SLOTS = 4 * NMF;
-  constexpr int NCOPY = XI + WI + SBI;               // copies per wave and step
+  constexpr int NCOPY = XI + WI;                     // copies per wave and step
   constexpr int PPW = BITS == 4 ? 4 : 8;             // dequant pieces per packed word
   constexpr int NPIECE = NT * G::WPL * PPW;          // dequant pieces per step
   static_assert(NCOPY <= 3 * NMF, "slot plan");  // (short tiles: several dequant pieces per slot)
@@ -513,13 +526,21 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     const unsigned char* xb = smem + xs * L::X;
     const unsigned char* xb1 = smem + xs1 * L::X;
     uint32_t lo[NT][G::WPL], hi[NT][G::WPL], c4[NT][G::WPL][4];  // split codes of the words being dequantized
+    // scale/bias block sb + 1 is copied during global step sb * SBK - 1, at
+    // the earliest one step after the prologue's reads (a first step at
+    // sb * SBK - 1 defers it to the next)
+    const int kq = (kt == 1 && (kb + 1) % SBK == 0) ? kb + 1 : kb + kt + 1;
+    const int sb_next = kq / SBK + 1;
+    const bool sb_now = kt >= 1 && kq % SBK == 0 && sb_next <= sb_last;
     static_for<SLOTS>([&](auto SI) {
       constexpr int sl = decltype(SI)::value;
       constexpr int j = sl / NMF, i = sl % NMF;
       constexpr int nt = i / MT, mt = i % MT;
       if constexpr (i == 0 && j == 3) {
         wait_lgkm0();
-        wait_vm<(NB - 2) * (VM_X + VM_W)>();
+        // (a step that copied a scale/bias block lets it stay in flight too)
+        if (sb_now) wait_vm<(NB - 2) * (VM_X + VM_W) + SBI>();
+        else wait_vm<(NB - 2) * (VM_X + VM_W)>();
         block_sync();
       }
       // matrix instruction (issued before the slot's LDS reads, so its operand
@@ -548,7 +569,11 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
         }
       });
 
-      // copies: copy q at slot q * (3 NMF) / NCOPY
+      // scale/bias block (every SBK steps), then copies: copy q at slot
+      // q * (3 NMF) / NCOPY
+      if constexpr (sl == 0) {
+        if (sb_now) issue_sb(sb_next);
+      }
       static_for<NCOPY>([&](auto QI) {
         constexpr int q = decltype(QI)::value;
         if constexpr (q * 3 * NMF / NCOPY == sl) {
