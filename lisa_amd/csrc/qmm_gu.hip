@@ -9,11 +9,6 @@
 
 namespace lisaq {
 
-#ifndef LISAQ_SHORT_NB
-#define LISAQ_SHORT_NB 3
-#endif
-constexpr int kShortNB = LISAQ_SHORT_NB;
-
 
 // Row tile: 256 rows when the average expert run is at least 192 rows (the
 // dequantized weights then serve twice the rows; measured at E = 128, k = 8,
@@ -53,7 +48,7 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
   LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
   LISAQ_REQUIRE(rows == 64 || rows == 128 || rows == 256, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built",
                 rows);
-  if (rows == 64) return gu_launch<2, kShortNB>(stream, p, bits, gs, grid);
+  if (rows == 64) return gu_launch<2>(stream, p, bits, gs, grid);
   return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
@@ -64,7 +59,7 @@ int qmm_gather_skip_launch(hipStream_t stream, const QmmParams& p, int bits, int
   qmm_fn fn = nullptr;
   int lds = 0;
   auto pick = [&](auto bt, auto mt) {
-    constexpr int B = decltype(bt)::value, MT = decltype(mt)::value, NB = MT == 2 ? kShortNB : 3;
+    constexpr int B = decltype(bt)::value, MT = decltype(mt)::value, NB = 3;
     lds = QmmLds<B, 64, MT, 1, 8, NB>::TOTAL;
     if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, false, NB, true>;
     if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, false, NB, true>;

@@ -122,6 +122,12 @@ __device__ __forceinline__ int x_lds_off(int row, int chunk) { return row * 128 
 // B-operand reads (lanes on 32 consecutive rows, one half) are conflict-free
 // in the same sense.
 __device__ __forceinline__ int w_swz(int row) { return ((row >> 2) ^ (row >> 3)) & 1; }
+// The W tile holds two K-steps per row (4-bit: 64 bytes = four 16-byte
+// chunks, logical chunk = 2 * step + half): physical chunk = logical ^
+// w_swz2(row), which puts any 8 consecutive rows' reads of one logical chunk
+// on 8 distinct 16-byte groups of a 128-byte line and any 16 on 16 distinct
+// groups of a 256-byte line.
+__device__ __forceinline__ int w_swz2(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 
 // 16 / 4 / 2 bytes per lane from global memory straight into LDS (lane l
 // writes lds + size*l; lds must be wave-uniform).
@@ -174,21 +180,21 @@ __device__ __forceinline__ void block_sync() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// NB: depth of the LDS rings (x of step k + NB - 1 and W of step k + NB are
-// in flight while step k runs)
+// NB: depth of the x ring (x of step k + NB - 1 in flight while step k runs).
+// W: two buffers of two K-steps each (the pair after next in flight).
 template <int BITS, int GS, int MT, int NT, int WN, int NB = 3, int WM = 1>
 struct QmmLds {
   static constexpr int BM = 32 * MT * WM, BN = WN * 32 * NT;
   static constexpr int RB = 32 / (32 / BITS) * 8;  // bytes of one W row per K-step (64 codes): 32 or 16
   static constexpr int X = BM / 8 * XG;            // x tile
-  static constexpr int W = BN * RB;                // packed W tile
-  static constexpr int WSTAGE = W;                 // packed W of one step
-  static constexpr int W0 = NB * X;                // W ring after the x ring
+  static constexpr int W = BN * RB;                // packed W of one K-step
+  static constexpr int WSTAGE = 2 * W;             // packed W of a pair of K-steps, [row][2 * RB]
+  static constexpr int W0 = NB * X;                // W buffers after the x ring
   // scales / biases: 8 consecutive groups of each row (16 bytes) per block,
   // two blocks (double-buffered), each [scales][biases]
   static constexpr int SBA = BN * 16;              // one array of one block
   static constexpr int SBB = 2 * SBA;              // one block
-  static constexpr int SB0 = W0 + NB * WSTAGE;     // the two blocks after the W ring
+  static constexpr int SB0 = W0 + 2 * WSTAGE;      // the two blocks after the W buffers
   static constexpr int TOTAL = SB0 + 2 * SBB;
 };
 
@@ -216,7 +222,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   using G = MGeo<BITS>;
   using L = QmmLds<BITS, GS, MT, NT, WN, NB, WM>;
   static_assert(WM == 1 || (!GU && !SKIP), "waves along M: plain tiles only");
-  static_assert(NB >= 3, "ring depth");
+  static_assert(NB == 3, "ring depth");
   constexpr int BM = L::BM;
   constexpr int BN = L::BN;
   constexpr int NWV = WN * WM;  // waves per workgroup
@@ -287,6 +293,12 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     m0 = (tile / gn) * BM;
   }
 
+  // K-steps of this workgroup: [kb, kb + nk) (the whole K unless split)
+  const int nk_all = p.K / BK;
+  const int per = (nk_all + ksplit - 1) / ksplit;
+  const int kb = split * per;
+  const int nk = nk_all - kb < per ? nk_all - kb : per;  // (host: every split has >= 1 step)
+
   // 32-row blocks of this tile that hold rows (the rest are clamped copies of
   // the last row and never stored): their matrix instructions are skipped
   const int mact = SKIP ? __builtin_amdgcn_readfirstlane(M - m0 >= BM ? MT : (M - m0 + 31) >> 5) : MT;
@@ -325,30 +337,35 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   uint32_t xvo[XI];  // byte offset of each x copy (the step's K offset goes in soffset)
 #pragma unroll
   for (int i = 0; i < XI; ++i) xvo[i] = xoff(i) * 2u;
-  // W: BN rows x RB bytes, row-major; 16 bytes per lane: WB bytes per wave in
-  // WI instructions (the last lanes idle when a wave's share is under 1 KB)
-  constexpr int WB = L::W / NWV;                  // bytes per wave
-  constexpr int WI = WB >= 1024 ? WB / 1024 : 1;  // instructions per wave
+  // W: a pair of K-steps per copy (2 * RB contiguous bytes of each row: per
+  // single step the 32 bytes of a row made every other lane of a copy touch
+  // its own cache line), BN rows x 2 RB bytes; 16 bytes per lane: WB bytes
+  // per wave in WI instructions (the last lanes idle when a wave's share is
+  // under 1 KB)
+  constexpr int WB = L::WSTAGE / NWV;             // bytes per wave and pair
+  constexpr int WI = WB >= 1024 ? WB / 1024 : 1;  // instructions per wave and pair
   constexpr int WLANES = WB >= 1024 ? 64 : WB / 16;
-  static_assert(L::W % NWV == 0 && (WB >= 1024 ? WB % 1024 == 0 : WB % 16 == 0), "W tile geometry");
+  constexpr int WROW = 2 * L::RB;                 // bytes of a row per pair
+  static_assert(L::WSTAGE % NWV == 0 && (WB >= 1024 ? WB % 1024 == 0 : WB % 16 == 0), "W tile geometry");
   const uint32_t rowbytes = (uint32_t)p.K * BITS / 8;
   const uint32_t wbytes = (uint32_t)p.N * rowbytes;
   // (GU: a wave's W share is rows of one stack -- WB bytes are whole rows of
   // one half of the tile -- so its descriptor is wave-uniform)
-  static_assert(!GU || (L::W / 2) % WB == 0, "gate|up W share");
-  const bool wup = GU && wave * WB >= L::W / 2;
+  static_assert(!GU || (L::WSTAGE / 2) % WB == 0, "gate|up W share");
+  const bool wup = GU && wave * WB >= L::WSTAGE / 2;
   const __amdgpu_buffer_rsrc_t rw = lds_rsrc(wup ? (const void*)w2 : (const void*)w, wbytes);
   uint32_t wvo[WI];
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
-    const int off = wave * WB + i * 1024 + lane * 16;  // byte in the W tile
-    int rr = off / L::RB;
+    const int off = wave * WB + i * 1024 + lane * 16;  // byte in the W pair buffer
+    const int row = off / WROW;
+    int rr = row;
     if (GU && rr >= BN / 2) rr -= BN / 2;
     int n = nt0 + rr;
     n = n < p.N ? n : p.N - 1;
-    // 4-bit: physical half (off / 16) % 2 of tile row off / 32 holds logical
-    // half ^ w_swz(row)
-    const int lb = BITS == 4 ? (off % L::RB) ^ (w_swz(off / L::RB) << 4) : off % L::RB;
+    // 4-bit: physical chunk (off / 16) % 4 of the row holds logical chunk
+    // physical ^ w_swz2(row)
+    const int lb = BITS == 4 ? (off % WROW) ^ (w_swz2(row) << 4) : off % WROW;
     wvo[i] = (uint32_t)n * rowbytes + (uint32_t)lb;
   }
   // scales / biases: blocks of 8 groups (SBK = GS / 8 K-steps), 16 bytes of
@@ -361,7 +378,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   constexpr int SBI = SI * 2 / NWV;            // scale/bias instructions per wave and block
   constexpr int SBK = GS / 8;                  // K-steps per block
   static_assert(SBI >= 1 && SI * 2 % NWV == 0 && SBK >= 2, "scale tile geometry");
-  constexpr int VM_X = XI, VM_W = WI;          // DMA instructions per wave and step: x tile, W stage
+  constexpr int VM_X = XI;                     // x copies per wave and step
   // copies i0 <= i < i1 of the x tile (i0, i1 compile-time after inlining)
   auto issue_x = [&](int k, int stage, int i0, int i1) {
     unsigned char* st = smem + stage * L::X;
@@ -386,15 +403,12 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     const int nb = nt0 + (up ? blk - SI / 2 : blk) * 64 + lane;
     sbrow[q] = (uint32_t)(nb < p.N ? nb : p.N - 1) * (uint32_t)p.G;
   }
-  // copy q of the W stage of step k
-  auto issue_w_part = [&](int k, int stage, int q) {
-    unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
-    const int k0 = k * BK;
-    if (WLANES == 64 || lane < WLANES) buf_lds16(rw, wvo[q], (uint32_t)k0 * BITS / 8, st + wave * WB + q * 1024);
-  };
-  auto issue_w = [&](int k, int stage) {
-#pragma unroll
-    for (int q = 0; q < WI; ++q) issue_w_part(k, stage, q);
+  // copy q of W pair pb (local K-steps 2 pb, 2 pb + 1, global kb + 2 pb ..)
+  // into pair buffer buf
+  auto issue_w_part = [&](int pb, int buf, int q) {
+    unsigned char* st = smem + L::W0 + buf * L::WSTAGE;
+    if (WLANES == 64 || lane < WLANES)
+      buf_lds16(rw, wvo[q], (uint32_t)(kb + 2 * pb) * L::RB, st + wave * WB + q * 1024);
   };
   // scale/bias block sb (groups 8 sb .. 8 sb + 7 of every row; past a row's
   // end: the next row's groups or zeros, never used) into block buffer sb % 2
@@ -415,19 +429,21 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     WV w[NT];
     uint16_t s[NT], b[NT];  // raw bf16 bits (converted where used)
   };
-  auto read_w = [&](int k, int stage, WLane& o) {
-    const unsigned char* st = smem + L::W0 + stage * L::WSTAGE;
+  // W of local step kl (clamped to the last step) from its pair buffer
+  auto read_w = [&](int kl, WLane& o) {
+    const unsigned char* st = smem + L::W0 + ((kl >> 1) & 1) * L::WSTAGE;
+    const int e = kl & 1;  // step within the pair
     // the lane's group (gs 32: the step's two groups, one per half-wave) and
     // its block buffer
-    const int g = k * BK / GS + (GS == 32 ? h : 0);
+    const int g = (kb + kl) * BK / GS + (GS == 32 ? h : 0);
     const unsigned char* sbb = smem + L::SB0 + ((g >> 3) & 1) * L::SBB + (g & 7) * 2;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int r = (wn * NT + nt) * 32 + col;
       o.s[nt] = *reinterpret_cast<const uint16_t*>(sbb + r * 16);
       o.b[nt] = *reinterpret_cast<const uint16_t*>(sbb + L::SBA + r * 16);
-      const int hp = BITS == 4 ? h ^ w_swz(r) : h;
-      o.w[nt] = *reinterpret_cast<const WV*>(st + r * L::RB + hp * (4 * G::WPL));
+      const int pc = BITS == 4 ? (2 * e + h) ^ w_swz2(r) : 2 * e + h;  // physical chunk (2-bit: 8 bytes)
+      o.w[nt] = *reinterpret_cast<const WV*>(st + r * WROW + pc * (4 * G::WPL));
     }
   };
   // s, b as f32 for one column tile of a W lane
@@ -451,17 +467,23 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x16{};
 
   // Pipeline.  Step k reads x stage k % 3 and its B operands (dequantized
-  // during step k-1), dequantizes step k+1's W (W stage (k+1) % 3, read from
-  // LDS one step earlier) into the other B buffer, and copies x(k+2) and
-  // W(k+3) into the stages freed by step k-1.  Copies past the last step
-  // re-read it, so every step issues the same number of copies and the waits
-  // are constants.
-  // K-steps of this workgroup: [kb, kb + nk) (the whole K unless split)
-  const int nk_all = p.K / BK;
-  const int per = (nk_all + ksplit - 1) / ksplit;
-  const int kb = split * per;
-  const int nk = nk_all - kb < per ? nk_all - kb : per;  // (host: every split has >= 1 step)
-  auto kc = [&](int k) { return kb + (k < nk ? k : nk - 1); };
+  // during step k-1), dequantizes step k+1's W (read from LDS one step
+  // earlier) into the other B buffer, and copies x(k+2) (and, odd steps, the
+  // W pair after next) into buffers whose last reads are behind a barrier.
+  // Copies past the last step re-read it, so the waits are constants per
+  // step parity.
+  auto kcl = [&](int k) { return k < nk ? k : nk - 1; };  // local step, clamped to the last
+  auto kc = [&](int k) { return kb + kcl(k); };            // global step, clamped
+  // W pairs (local steps 2 pb, 2 pb + 1) in buffer pb % 2: pairs 0 and 1 in
+  // the prologue, pair b + 1 during local step 2 b - 1 (after the last read
+  // of pair b - 1, at step 2 b - 3, and landed before the first read of pair
+  // b + 1, at step 2 b); a pair past the last re-reads the last into the other
+  // buffer (never read)
+  const int pb_last = (nk - 1) >> 1;
+  auto issue_wpair = [&](int pb, int buf) {
+#pragma unroll
+    for (int q = 0; q < WI; ++q) issue_w_part(pb < pb_last ? pb : pb_last, buf, q);
+  };
   uint32_t bA[NT][16], bB[NT][16];  // B operands of the current / next step
   // scale/bias blocks: the first two in the prologue; block sb + 1 during
   // step sb * SBK - 1 (global steps), after the last read of block sb - 1
@@ -471,23 +493,14 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   issue_sb(kb / SBK);
   if (kb / SBK + 1 <= sb_last) issue_sb(kb / SBK + 1);
   issue_x(kc(0), 0, 0, XI);
-  issue_w(kc(0), 0);
-  issue_w(kc(1), 1);
-  if constexpr (NB == 3) {
-    issue_x(kc(1), 1, 0, XI);
-    issue_w(kc(2), 2);
-  } else {
-    static_for<NB - 2>([&](auto I) {
-      constexpr int i = decltype(I)::value + 1;
-      issue_x(kc(i), i, 0, XI);
-      issue_w(kc(i + 1), i + 1);
-    });
-  }
-  wait_vm<(NB - 2) * (VM_X + VM_W)>();  // x(0), W(0), W(1) landed (this wave's part)
+  issue_wpair(0, 0);
+  issue_wpair(1, 1);
+  issue_x(kc(1), 1, 0, XI);
+  wait_vm<VM_X>();  // x(0), W pairs 0 and 1 landed (this wave's part)
   block_sync();
   {
     WLane w0;
-    read_w(kc(0), 0, w0);
+    read_w(kcl(0), w0);
     dequant_all(w0, bA);
   }
   auto read_a1 = [&](const unsigned char* xb, int j, int mt) -> u32x4 {
@@ -497,7 +510,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   WLane wA, wB;  // W of the step after the current one (alternating)
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) a0[mt] = read_a1(smem, 0, mt);
-  read_w(kc(1), 1, wA);
+  read_w(kcl(1), wA);
 
   // One step as 4 * MT * NT slots, each one matrix instruction plus its share
   // of the other work, in program order (scheduling barriers between slots):
@@ -509,20 +522,20 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   //  * the dequantization of the next step's W is cut into pieces of one
   //    bf16 pair (about five VALU ops) spread evenly over all slots, so the
   //    VALU work hides under the matrix instructions;
-  //  * between sub-steps 2 and 3: wait for x(k+1), W(k+2) and for this
-  //    step's LDS reads, then the workgroup barrier.
+  //  * between sub-steps 2 and 3: wait for x(k+1), the W pair of step k+2
+  //    and for this step's LDS reads, then the workgroup barrier.
+  // Odd (local) steps also copy a W pair.
   constexpr int NMF = MT * NT;
   constexpr int SLOTS = 4 * NMF;
-  constexpr int NCOPY = XI + WI;                     // copies per wave and step
   constexpr int PPW = BITS == 4 ? 4 : 8;             // dequant pieces per packed word
   constexpr int NPIECE = NT * G::WPL * PPW;          // dequant pieces per step
-  static_assert(NCOPY <= 3 * NMF, "slot plan");  // (short tiles: several dequant pieces per slot)
-  int xs = 0, ws1 = 1;  // x stage of step k, W stage of step k+1
-  auto step = [&](int kt, uint32_t (*bcur)[16], uint32_t (*bnxt)[16], const WLane& wn, WLane& wnn) {
+  static_assert(XI + WI <= 3 * NMF, "slot plan");  // (short tiles: several dequant pieces per slot)
+  int xs = 0;  // x stage of step k
+  auto step = [&](int kt, auto odd, uint32_t (*bcur)[16], uint32_t (*bnxt)[16], const WLane& wn, WLane& wnn) {
+    constexpr bool ODD = decltype(odd)::value;
+    constexpr int NCOPY = XI + (ODD ? WI : 0);  // copies per wave in this step
     const int xs2 = xs == 0 ? NB - 1 : xs - 1;    // (k+NB-1) % NB: x copy of this step
-    const int ws3 = ws1 == 0 ? NB - 1 : ws1 - 1;  // (k+NB) % NB = k % NB: W copy of this step
     const int xs1 = xs == NB - 1 ? 0 : xs + 1;    // (k+1) % NB
-    const int ws2 = ws1 == NB - 1 ? 0 : ws1 + 1;  // (k+2) % NB
     const unsigned char* xb = smem + xs * L::X;
     const unsigned char* xb1 = smem + xs1 * L::X;
     uint32_t lo[NT][G::WPL], hi[NT][G::WPL], c4[NT][G::WPL][4];  // split codes of the words being dequantized
@@ -539,8 +552,8 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
       if constexpr (i == 0 && j == 3) {
         wait_lgkm0();
         // (a step that copied a scale/bias block lets it stay in flight too)
-        if (sb_now) wait_vm<(NB - 2) * (VM_X + VM_W) + SBI>();
-        else wait_vm<(NB - 2) * (VM_X + VM_W)>();
+        if (sb_now) wait_vm<NCOPY + SBI>();
+        else wait_vm<NCOPY>();
         block_sync();
       }
       // matrix instruction (issued before the slot's LDS reads, so its operand
@@ -555,7 +568,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
       __builtin_amdgcn_sched_barrier(0);
       // the W words of the step after next, first thing after the barrier (the
       // next step's first dequantization piece needs them)
-      if constexpr (j == 3 && i == 0) read_w(kc(kt + 2), ws2, wnn);
+      if constexpr (j == 3 && i == 0) read_w(kcl(kt + 2), wnn);
       // A operands of the next sub-step, two per slot in the sub-step's first
       // slots: they have landed by the sub-step's end (where the compiler
       // waits for all outstanding LDS reads)
@@ -577,8 +590,12 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
       static_for<NCOPY>([&](auto QI) {
         constexpr int q = decltype(QI)::value;
         if constexpr (q * 3 * NMF / NCOPY == sl) {
-          if constexpr (q < XI) issue_x(kc(kt + NB - 1), xs2, q, q + 1);
-          else issue_w_part(kc(kt + NB), ws3, q - XI);
+          if constexpr (q < XI) {
+            issue_x(kc(kt + NB - 1), xs2, q, q + 1);
+          } else {
+            const int pn = (kt + 1) / 2 + 1;  // the pair after next
+            issue_w_part(pn < pb_last ? pn : pb_last, pn & 1, q - XI);
+          }
         }
       });
       // dequant pieces: piece d at slot d * SLOTS / NPIECE
@@ -609,15 +626,14 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
       __builtin_amdgcn_sched_barrier(0);
     });
     xs = xs1;
-    ws1 = ws2;
   };
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
-    step(kt, bA, bB, wA, wB);
-    step(kt + 1, bB, bA, wB, wA);
+    step(kt, std::false_type{}, bA, bB, wA, wB);
+    step(kt + 1, std::true_type{}, bB, bA, wB, wA);
   }
   if (kt < nk) {
-    step(kt, bA, bB, wA, wB);
+    step(kt, std::false_type{}, bA, bB, wA, wB);
   }
 
   // epilogue: the accumulator of (mt, nt) is y^T: lane holds row m = col of
