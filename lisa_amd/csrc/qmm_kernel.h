@@ -612,14 +612,17 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
             }
             // (one v_perm and two v_fma_mix per pair instead of two
             // conversions and two fmas: 18 VALU per word instead of 22)
-            bnxt[dnt][dw * 4 + dp] = deq_pair(pair_bytes<dp>(lo[dnt][dw], hi[dnt][dw]), s_ * 16777216.0f, b_);
+            // (opaque: pinned to its slot -- a branch later in the step, such
+            // as the conditional wait, otherwise lets the compiler sink the
+            // pieces together next to it, out from under the matrix work)
+            bnxt[dnt][dw * 4 + dp] = opaque(deq_pair(pair_bytes<dp>(lo[dnt][dw], hi[dnt][dw]), s_ * 16777216.0f, b_));
           } else {
             if constexpr (dp == 0) {
 #pragma unroll
               for (int c = 0; c < 4; ++c) c4[dnt][dw][c] = opaque((wv >> (2 * c)) & 0x03030303u);
             }
             constexpr int m = dp / 2, e = (dp % 2) * 2;
-            bnxt[dnt][dw * 8 + dp] = deq_pair(pair_bytes<m>(c4[dnt][dw][e], c4[dnt][dw][e + 1]), s_ * 16777216.0f, b_);
+            bnxt[dnt][dw * 8 + dp] = opaque(deq_pair(pair_bytes<m>(c4[dnt][dw][e], c4[dnt][dw][e + 1]), s_ * 16777216.0f, b_));
           }
         }
       });
