@@ -337,13 +337,13 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
     p.K = (int)K;
     p.G = (int)(K / gs);
     if (L.qmm_cap > 0) {
-      rc = L.mc.MT == 8 ? qmm_gather_skip_launch(st, p, bits, gs, L.qmm_cap, 256)
+      rc = L.mc.MT == 8 ? qmm_gather_launch(st, p, bits, gs, L.qmm_cap, 256)
                         : qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
       if (rc) return rc;
     }
     if (L.qs_cap > 0) {
       p.tiles = (const int4*)(base + L.qs_off);
-      if ((rc = qmm_gather_skip_launch(st, p, bits, gs, L.qs_cap, kShortBM))) return rc;
+      if ((rc = qmm_gather_launch(st, p, bits, gs, L.qs_cap, kShortBM))) return rc;
     }
   }
   return LISAQ_OK;

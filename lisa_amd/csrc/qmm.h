@@ -46,8 +46,8 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
 constexpr int kGuBN = 128;          // output-column tile of qmm_gu_launch
 int qmm_gu_rows(int64_t R, int E);  // its row tile for R sorted rows over E experts
 // Gather (tile-table) launch of `rows`-row tiles (256, or 64 for the short
-// last tiles of runs) that skip their empty 32-row blocks.
-int qmm_gather_skip_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows);
+// last tiles of runs).
+int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows);
 // Row tile of the short-tile tables: a run's last tile goes there when it holds
 // at most this many rows.  Its rows are bitwise equal to the same rows in a
 // taller tile (the accumulation order does not depend on the tile height).

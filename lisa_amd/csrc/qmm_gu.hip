@@ -9,6 +9,14 @@
 
 namespace lisaq {
 
+// Tile-table kernels skip the matrix instructions of 32-row blocks past a
+// tile's rows only in the 64-row short tiles (a run's last tile, often one
+// block of two): in the taller tiles, whose runs mostly fill them, the
+// per-instruction branches cost more than the skipped work (MoE E = 128,
+// k = 8, H = 2048, I = 768: T = 4096 501 -> 494 us, T = 512 178 -> 167 us;
+// no skipping anywhere: 498 / 172 us).
+constexpr bool kSkip(int mt) { return mt <= 2; }
+
 
 // Row tile: 256 rows when the average expert run is at least 192 rows (the
 // dequantized weights then serve twice the rows; measured at E = 128, k = 8,
@@ -23,9 +31,9 @@ static int gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, i
   qmm_fn fn = nullptr;
   auto pick = [&](auto bt) {
     constexpr int B = decltype(bt)::value;
-    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, true, NB>;
-    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, true, NB>;
-    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, true, NB>;
+    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, true, NB, kSkip(MT)>;
+    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, true, NB, kSkip(MT)>;
+    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, true, NB, kSkip(MT)>;
   };
   if (bits == 4) pick(std::integral_constant<int, 4>{});
   if (bits == 2) pick(std::integral_constant<int, 2>{});
@@ -52,18 +60,18 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
   return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
-// Gather launches whose 32-row blocks past a tile's rows skip their matrix
-// instructions: 256-row tiles (the MoE prefill's down projection when runs
-// average >= 192 rows) and 64-row tiles (the short last tile of a run).
-int qmm_gather_skip_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows) {
+// Gather launches of 256-row tiles (the MoE prefill's down projection when
+// runs average >= 192 rows) and of 64-row tiles (the short last tile of a
+// run, skipping the matrix instructions of an empty 32-row block).
+int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows) {
   qmm_fn fn = nullptr;
   int lds = 0;
   auto pick = [&](auto bt, auto mt) {
     constexpr int B = decltype(bt)::value, MT = decltype(mt)::value, NB = 3;
     lds = QmmLds<B, 64, MT, 1, 8, NB>::TOTAL;
-    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, false, NB, true>;
-    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, false, NB, true>;
-    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, false, NB, true>;
+    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, false, NB, kSkip(MT)>;
+    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, false, NB, kSkip(MT)>;
+    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, false, NB, kSkip(MT)>;
   };
   LISAQ_REQUIRE(rows == 64 || rows == 256, LISAQ_EUNSUPPORTED, "qmm gather: row tile %d not built", rows);
   auto pick_mt = [&](auto bt) {
