@@ -722,9 +722,11 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     }
   };
   if constexpr (WM == 1) {
-    if (whole && !p.tiles && (p.N & 7) == 0) {
-      // (plain launches: a gather tile is often a few rows, which the direct
-      // stores below serve for less)
+    if (whole && (!p.tiles || MT >= 8) && (p.N & 7) == 0) {
+      // (plain launches and 256-row gather tiles, which runs mostly fill --
+      // a run's short last tile goes to the 64-row kernel: MoE T = 4096
+      // 500 -> 478 us; a 128-row gather tile is often a few rows, which the
+      // direct stores below serve for less)
       // whole tile through LDS, RB rows at a time ([RB][BN + 8] bf16, 16 bytes
       // of padding per row), then 16-byte stores along the output rows (a
       // row of the tile is BN * 2 contiguous bytes of y), after every copy into
