@@ -172,6 +172,7 @@ struct GatherLayout {
   size_t qmm_off, qs_off, total;
   QmmConfig mc;
   bool mm() const { return qmm_cap > 0 || qs_cap > 0; }  // any matmul tiles
+  int short_bn() const { return gu ? kShortBN / 2 : kShortBN; }  // output columns of a short tile
 };
 
 static size_t up256(size_t v) { return (v + 255) / 256 * 256; }
@@ -262,7 +263,7 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   const bool short_ok = mm && L.mc.BM > kShortBM && path_int("LISAQ_GATHER_SHORT", 1) != 0;
   const int64_t ntbn = (N + L.mc.BN - 1) / L.mc.BN;
   L.qmm_cap = (mm && !(short_ok && mr <= kShortBM)) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ntbn) : 0;
-  L.qs_cap = short_ok ? (int)(runs * ntbn) : 0;
+  L.qs_cap = short_ok ? (int)(runs * ((N + L.short_bn() - 1) / L.short_bn())) : 0;
   L.qmm_off = o;
   L.qs_off = L.qmm_off + up256((size_t)L.qmm_cap * 16);
   L.total = L.qs_off + up256((size_t)L.qs_cap * 16);
@@ -287,6 +288,7 @@ static TileTableJob gather_job(const GatherLayout& L, int64_t N, void* ws) {
   j.qmm_tab = (int4*)(base + L.qmm_off);
   j.qmm_cap = L.qmm_cap;
   j.SBM = kShortBM;
+  j.SBN = L.short_bn();
   j.qs_tab = L.qs_cap ? (int4*)(base + L.qs_off) : nullptr;
   j.qs_cap = L.qs_cap;
   j.counts = (int32_t*)base;
@@ -767,8 +769,8 @@ static int64_t gu_cap(int64_t R, int64_t I, int E) {
 }
 static int64_t gu_short_cap(int64_t R, int64_t I, int E) {
   const int64_t runs = R < E ? R : E;
-  return qmm_gu_rows(R, E) > kShortBM && path_int("LISAQ_GATHER_SHORT", 1) != 0 ? runs * ((I + kGuBN - 1) / kGuBN)
-                                                                               : 0;
+  constexpr int sbn = kShortBN / 2;  // output columns of a short gate|up tile
+  return qmm_gu_rows(R, E) > kShortBM && path_int("LISAQ_GATHER_SHORT", 1) != 0 ? runs * ((I + sbn - 1) / sbn) : 0;
 }
 // workspace of the gate|up tables: [counts 256 B][tiles][short tiles]
 static size_t gu_ws_bytes(int64_t R, int64_t I, int E) {
@@ -799,6 +801,7 @@ static TileTableJob gu_job(int64_t R, int64_t I, int E, void* ws) {
   j.qmm_tab = (int4*)(gb + 256);
   j.qmm_cap = (int)gu_cap(R, I, E);
   j.SBM = kShortBM;
+  j.SBN = kShortBN / 2;
   j.qs_cap = (int)gu_short_cap(R, I, E);
   j.qs_tab = j.qs_cap ? (int4*)(gb + 256 + up256((size_t)j.qmm_cap * 16)) : nullptr;
   j.counts = (int32_t*)gb;

@@ -36,12 +36,12 @@ constexpr int kTileTableMaxExperts = 16384;
 // `limit` as matvec tiles, of mv_vr[0] output rows in table mv_tab[0] when
 // they hold at most MV rows, else of mv_vr[1] rows in mv_tab[1]; the others as
 // BM x BN matmul tiles; with a short table (qs_tab, SBM > 0) the last tile of
-// a run goes there, as an SBM x BN tile, when it holds at most SBM rows.
+// a run goes there, as SBM x SBN tiles, when it holds at most SBM rows.
 // Entries past a matvec table's count are written as {-1,..} for mv_pad[j]
 // entries (its launch grid), the matmul tables' up to their capacity.
 // counts[0..2]: matvec tiles, matmul tiles, overflow/bad-ids flag.
 struct TileTableJob {
-  int N, limit, MV, BM, BN, SBM;
+  int N, limit, MV, BM, BN, SBM, SBN;
   int4* mv_tab[2];
   int mv_cap[2], mv_pad[2], mv_vr[2];
   int4* qmm_tab;

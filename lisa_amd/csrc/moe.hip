@@ -632,6 +632,7 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   const int nv0 = (N + job.mv_vr[0] - 1) / job.mv_vr[0];
   const int nv1 = (N + job.mv_vr[1] - 1) / job.mv_vr[1];
   const int ntbn = (N + BN - 1) / BN;
+  const int ntsb = SBM ? (N + job.SBN - 1) / job.SBN : 0;  // short tiles per run
   const int chunk = (E + 1023) / 1024;
   const int e0 = tid * chunk, e1 = e0 + chunk < E ? e0 + chunk : E;
   int c[4] = {0, 0, 0, 0};
@@ -642,7 +643,7 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
       const int rem = len % BM;
       const bool sh = rem > 0 && rem <= SBM;
       c[2] += (len / BM + (rem > 0 && !sh ? 1 : 0)) * ntbn;
-      c[3] += sh ? ntbn : 0;
+      c[3] += sh ? ntsb : 0;
     } else if (len <= MV) c[0] += nv0;
     else c[1] += nv1;
   }
@@ -691,7 +692,7 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
           const bool sh = rows <= SBM;  // (SBM < BM: only a run's last tile)
           int4* tab = sh ? job.qs_tab : qmm_tab;
           int& oq = o[sh ? 3 : 2];
-          for (int nt = 0; nt < ntbn; ++nt, ++oq)
+          for (int nt = 0; nt < (sh ? ntsb : ntbn); ++nt, ++oq)
             if (oq < caps[sh ? 3 : 2]) tab[oq] = make_int4(e, st + r0, rows, nt);
         }
       } else if (len <= MV) {

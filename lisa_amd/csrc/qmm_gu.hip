@@ -26,26 +26,27 @@ int qmm_gu_rows(int64_t R, int E) {
   return tune_int("LISAQ_GU_ROWS", R >= 192 * (int64_t)E ? 256 : 128);
 }
 
-template <int MT, int NB = 3>
+template <int MT, int WN = 8, int NB = 3>
 static int gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid) {
   qmm_fn fn = nullptr;
   auto pick = [&](auto bt) {
     constexpr int B = decltype(bt)::value;
-    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, true, NB, kSkip(MT)>;
-    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, true, NB, kSkip(MT)>;
-    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, true, NB, kSkip(MT)>;
+    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, WN, false, true, NB, kSkip(MT)>;
+    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, WN, false, true, NB, kSkip(MT)>;
+    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, WN, false, true, NB, kSkip(MT)>;
   };
   if (bits == 4) pick(std::integral_constant<int, 4>{});
   if (bits == 2) pick(std::integral_constant<int, 2>{});
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmm_gu: bits=%d group_size=%d not supported", bits, gs);
   // the 4-bit ring's size at either code width: the epilogue's gate|up
   // exchange needs that much
-  constexpr int lds = QmmLds<4, 64, MT, 1, 8, NB>::TOTAL;
-  static_assert(lds >= QmmLds<2, 64, MT, 1, 8, NB>::TOTAL && lds <= 160 * 1024, "ring size");
-  static_assert(kGuBN == QmmLds<4, 64, MT, 1, 8>::BN / 2, "gate|up output tile");
+  constexpr int lds = QmmLds<4, 64, MT, 1, WN, NB>::TOTAL;
+  static_assert(lds >= QmmLds<2, 64, MT, 1, WN, NB>::TOTAL && lds <= 160 * 1024, "ring size");
+  static_assert(MT == 2 ? kShortBN == QmmLds<4, 64, MT, 1, WN>::BN : kGuBN == QmmLds<4, 64, MT, 1, WN>::BN / 2,
+                "gate|up output tile");
   if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm_gu")) return rc;
   if (grid <= 0) return LISAQ_OK;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(512), lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * WN), lds, stream, p);
   return check_launch("qmm_gu");
 }
 
@@ -56,7 +57,7 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
   LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
   LISAQ_REQUIRE(rows == 64 || rows == 128 || rows == 256, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built",
                 rows);
-  if (rows == 64) return gu_launch<2>(stream, p, bits, gs, grid);
+  if (rows == 64) return gu_launch<2, kShortWN>(stream, p, bits, gs, grid);
   return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
@@ -65,13 +66,16 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
 // run, skipping the matrix instructions of an empty 32-row block).
 int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows) {
   qmm_fn fn = nullptr;
-  int lds = 0;
+  int lds = 0, threads = 512;
   auto pick = [&](auto bt, auto mt) {
     constexpr int B = decltype(bt)::value, MT = decltype(mt)::value, NB = 3;
-    lds = QmmLds<B, 64, MT, 1, 8, NB>::TOTAL;
-    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, 8, false, false, NB, kSkip(MT)>;
-    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, 8, false, false, NB, kSkip(MT)>;
-    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, 8, false, false, NB, kSkip(MT)>;
+    constexpr int WN = MT == 2 ? kShortWN : 8;
+    static_assert(MT != 2 || QmmLds<B, 64, MT, 1, WN, NB>::BN == kShortBN, "short tile width");
+    lds = QmmLds<B, 64, MT, 1, WN, NB>::TOTAL;
+    threads = 64 * WN;
+    if (gs == 32) fn = qmm_kernel<B, 32, MT, 1, WN, false, false, NB, kSkip(MT)>;
+    if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, WN, false, false, NB, kSkip(MT)>;
+    if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, WN, false, false, NB, kSkip(MT)>;
   };
   LISAQ_REQUIRE(rows == 64 || rows == 256, LISAQ_EUNSUPPORTED, "qmm gather: row tile %d not built", rows);
   auto pick_mt = [&](auto bt) {
@@ -86,7 +90,7 @@ int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, 
                 LISAQ_EINVAL_SHAPE, "qmm gather: x or one weight matrix too large");
   if (int rc = allow_dyn_lds((const void*)fn, lds, "qmm_gather")) return rc;
   if (grid <= 0) return LISAQ_OK;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(512), lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), lds, stream, p);
   return check_launch("qmm_gather");
 }
 
