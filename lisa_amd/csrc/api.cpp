@@ -184,7 +184,7 @@ constexpr int kGatherMvRows = 16;
 // knows one (moe_forward: a token picks an expert at most once, so T);
 // otherwise R.  It only sizes the matvec rows and decides if matmul tiles can
 // occur; the tables still follow the actual runs.
-// tall: matmul tiles of 256 rows (runs known to average >= 192 rows).
+// tall: matmul tiles of kTallBM rows (runs known to average >= 192 rows).
 // gu: tables for gate|up + SwiGLU (N = I): matvec entries of half a block's
 // rows (the other half of its waves take the up weights), matmul tiles of the
 // gate|up matmul kernel.
@@ -245,8 +245,8 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   }
   L.mc = qmm_config(L.limit, N, K, gs, bits);
   {
-    const int mt = tall ? 8 : tune_int("LISAQ_GATHER_MT", L.mc.MT);
-    if (mt == 4 || mt == 6 || mt == 8) {
+    const int mt = tall ? kTallBM / 32 : tune_int("LISAQ_GATHER_MT", L.mc.MT);
+    if (mt == 4 || mt == 6 || mt == 8 || mt == kTallBM / 32) {
       L.mc.MT = mt;
       L.mc.BM = 32 * mt;
     }
@@ -339,8 +339,8 @@ static int gather_launch(hipStream_t st, const GatherLayout& L, const void* x, c
     p.K = (int)K;
     p.G = (int)(K / gs);
     if (L.qmm_cap > 0) {
-      rc = L.mc.MT == 8 ? qmm_gather_launch(st, p, bits, gs, L.qmm_cap, 256)
-                        : qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
+      rc = L.mc.MT == kTallBM / 32 ? qmm_gather_launch(st, p, bits, gs, L.qmm_cap, kTallBM)
+                                   : qmm_launch(st, L.mc, p, bits, gs, L.qmm_cap, 1);
       if (rc) return rc;
     }
     if (L.qs_cap > 0) {
@@ -926,7 +926,7 @@ struct MoeLayout {
   size_t idx, wts, sorted, order, rows, inv, offs, hist, xs, g, u, d, gws, total;
 };
 
-// The down projection of the fused-gate|up prefill takes 256-row matmul
+// The down projection of the fused-gate|up prefill takes kTallBM-row matmul
 // tiles when runs average >= 192 rows (as the gate|up matmul does).
 static bool moe_down_tall(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
   return moe_gu_path(T, H, I, E, k, gs, bits) && tune_int("LISAQ_MOE_DOWN_TALL", 1) != 0 &&

@@ -52,6 +52,9 @@ int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, 
 // at most this many rows.  Its rows are bitwise equal to the same rows in a
 // taller tile (the accumulation order does not depend on the tile height).
 constexpr int kShortBM = 64;
+// Row tile of the tall gather launches (runs averaging >= 192 rows: gate|up
+// and down of the MoE prefill): 288 rows, nine 32-row blocks
+constexpr int kTallBM = 288;
 // (four waves, 128 columns: MoE T = 4096 471 -> 476 us, T = 512 173 -> 180 us)
 constexpr int kShortWN = 8;  // waves of a short-tile workgroup (32 columns each)
 constexpr int kShortBN = 32 * kShortWN;   // output columns of a short tile (gate|up: half of them)

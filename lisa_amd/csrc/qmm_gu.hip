@@ -1,5 +1,5 @@
 // Gate|up matmul of the MoE prefill (the qmm kernel with GU = true): one
-// launch computes both expert projections of each 128- or 256-row x 128-column
+// launch computes both expert projections of each 64-, 128- or 288-row x 128-column
 // tile,
 // reads the tile's x rows through the sort's row map, and writes SwiGLU of the
 // two -- the reference's gather_qmm(gate), gather_qmm(up), swiglu sequence
@@ -15,15 +15,19 @@ namespace lisaq {
 // per-instruction branches cost more than the skipped work (MoE E = 128,
 // k = 8, H = 2048, I = 768: T = 4096 501 -> 494 us, T = 512 178 -> 167 us;
 // no skipping anywhere: 498 / 172 us).
-constexpr bool kSkip(int mt) { return mt <= 2; }
+// The 288-row tiles skip too: without the branches the compiler spills
+// registers (their 256 VGPRs hold nine 32-row blocks of accumulators).
+constexpr bool kSkip(int mt) { return mt <= 2 || mt == 9; }
 
 
-// Row tile: 256 rows when the average expert run is at least 192 rows (the
-// dequantized weights then serve twice the rows; measured at E = 128, k = 8,
-// H = 2048, I = 768: T = 4096 313 vs 330 us), else 128 rows (T = 512: 97 vs
-// 131 us, most runs fit one 128-row tile).
+// Row tile: 288 rows when the average expert run is at least 192 rows (the
+// dequantized weights then serve more rows; measured at E = 128, k = 8,
+// H = 2048, I = 768: T = 4096 313 vs 330 us with 256- against 128-row tiles;
+// 288 rows take a run of 256 + a few rows in one tile instead of a full tile
+// and a short one), else 128 rows (T = 512: 97 vs 131 us, most runs fit one
+// 128-row tile).
 int qmm_gu_rows(int64_t R, int E) {
-  return tune_int("LISAQ_GU_ROWS", R >= 192 * (int64_t)E ? 256 : 128);
+  return tune_int("LISAQ_GU_ROWS", R >= 192 * (int64_t)E ? kTallBM : 128);
 }
 
 template <int MT, int WN = 8, int NB = 3>
@@ -55,13 +59,14 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
   LISAQ_REQUIRE((int64_t)p.N * p.K * bits / 8 < ((int64_t)1 << 32), LISAQ_EINVAL_SHAPE,
                 "qmm_gu: one weight matrix larger than 4 GiB");
   LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
-  LISAQ_REQUIRE(rows == 64 || rows == 128 || rows == 256, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built",
-                rows);
+  LISAQ_REQUIRE(rows == 64 || rows == 128 || rows == 256 || rows == 288, LISAQ_EUNSUPPORTED,
+                "qmm_gu: row tile %d not built", rows);
   if (rows == 64) return gu_launch<2, kShortWN>(stream, p, bits, gs, grid);
+  if (rows == 288) return gu_launch<9>(stream, p, bits, gs, grid);
   return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
-// Gather launches of 256-row tiles (the MoE prefill's down projection when
+// Gather launches of 288-row tiles (the MoE prefill's down projection when
 // runs average >= 192 rows) and of 64-row tiles (the short last tile of a
 // run, skipping the matrix instructions of an empty 32-row block).
 int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int grid, int rows) {
@@ -77,9 +82,11 @@ int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, 
     if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, WN, false, false, NB, kSkip(MT)>;
     if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, WN, false, false, NB, kSkip(MT)>;
   };
-  LISAQ_REQUIRE(rows == 64 || rows == 256, LISAQ_EUNSUPPORTED, "qmm gather: row tile %d not built", rows);
+  LISAQ_REQUIRE(rows == 64 || rows == 256 || rows == 288, LISAQ_EUNSUPPORTED, "qmm gather: row tile %d not built",
+                rows);
   auto pick_mt = [&](auto bt) {
-    if (rows == 256) pick(bt, std::integral_constant<int, 8>{});
+    if (rows == 288) pick(bt, std::integral_constant<int, 9>{});
+    else if (rows == 256) pick(bt, std::integral_constant<int, 8>{});
     else pick(bt, std::integral_constant<int, 2>{});
   };
   if (bits == 4) pick_mt(std::integral_constant<int, 4>{});

@@ -305,13 +305,20 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
 
   // ---- global -> LDS copies of one K-step (all direct-to-LDS; rows past the
   // matrix are clamped to the last one, their results are never stored)
-  // x: BM/8 instructions of 1 KB, XI per wave; lane l fills row 8g + l/8,
+  // x: BM/8 instructions of 1 KB (row groups g of 8 rows), XI per wave -- or,
+  // when they do not divide evenly (288-row tiles: 36 over 8 waves), XI for
+  // the first XLONG waves and XI - 1 for the others; lane l fills row 8g + l/8,
   // physical chunk l%8 (= logical chunk (l%8) ^ x_swz(row), and x_swz(row) =
   // l/8 ^ (g % 2))
-  constexpr int XI = BM / 8 / NWV;
+  constexpr int XGT = BM / 8;                  // row groups of the tile
+  constexpr int XI = (XGT + NWV - 1) / NWV;    // copies of the busiest waves
+  constexpr int XLONG = XGT - (XI - 1) * NWV;  // waves with XI copies (NWV: all)
+  constexpr bool XUNEVEN = XLONG != NWV;
+  const bool xshort = XUNEVEN && wave >= XLONG;  // (wave-uniform) XI - 1 copies
+  const int xg0 = wave < XLONG ? wave * XI : XLONG * XI + (wave - XLONG) * (XI - 1);  // first row group
   // element offsets, recomputed per copy to save registers (the host checks
   // that x fits 2^31 elements)
-  const int xrow0 = m0 + wave * XI * 8 + (lane >> 3);
+  const int xrow0 = m0 + xg0 * 8 + (lane >> 3);
   const uint32_t xchunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 3);
   uint32_t xsrc[GU ? XI : 1];  // GU: element offset of each copy's gathered x row
   if constexpr (GU) {
@@ -324,10 +331,10 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   }
   auto xoff = [&](int i) -> uint32_t {
     if constexpr (GU) {
-      return xsrc[i] + (xchunk ^ (((wave * XI + i) & 1) << 3));
+      return xsrc[i] + (xchunk ^ (((xg0 + i) & 1) << 3));
     } else {
       const int row = xrow0 + 8 * i < M ? xrow0 + 8 * i : M - 1;
-      return (uint32_t)row * (uint32_t)p.K + (xchunk ^ (((wave * XI + i) & 1) << 3));
+      return (uint32_t)row * (uint32_t)p.K + (xchunk ^ (((xg0 + i) & 1) << 3));
     }
   };
   // byte ranges of the copies' descriptors (every offset stays below 2^32:
@@ -385,7 +392,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     const uint32_t k0 = (uint32_t)k * BK;
 #pragma unroll
     for (int i = 0; i < XI; ++i)
-      if (i >= i0 && i < i1) buf_lds16(rx, xvo[i], k0 * 2u, st + (wave * XI + i) * XG);
+      if (i >= i0 && i < i1 && (i < XI - 1 || !xshort)) buf_lds16(rx, xvo[i], k0 * 2u, st + (xg0 + i) * XG);
   };
   // scale/bias copies: the wave's descriptor (wave-uniform: which array, which
   // stack) and each lane's row offset nb * G
@@ -496,7 +503,9 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   issue_wpair(0, 0);
   issue_wpair(1, 1);
   issue_x(kc(1), 1, 0, XI);
-  wait_vm<VM_X>();  // x(0), W pairs 0 and 1 landed (this wave's part)
+  // x(0), W pairs 0 and 1 landed (this wave's part; x(1) may be in flight)
+  if (xshort) wait_vm<(VM_X > 1 ? VM_X - 1 : 0)>();
+  else wait_vm<VM_X>();
   block_sync();
   {
     WLane w0;
@@ -552,8 +561,14 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
       if constexpr (i == 0 && j == 3) {
         wait_lgkm0();
         // (a step that copied a scale/bias block lets it stay in flight too)
-        if (sb_now) wait_vm<NCOPY + SBI>();
-        else wait_vm<NCOPY>();
+        // (a wave with one x copy fewer lets one fewer stay in flight)
+        if (xshort) {
+          if (sb_now) wait_vm<NCOPY - 1 + SBI>();
+          else wait_vm<NCOPY - 1>();
+        } else {
+          if (sb_now) wait_vm<NCOPY + SBI>();
+          else wait_vm<NCOPY>();
+        }
         block_sync();
       }
       // matrix instruction (issued before the slot's LDS reads, so its operand
@@ -651,7 +666,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
     // [2][RB][BN/2 + 8] bf16, gate rows then up rows, 16 bytes of padding per
     // row against bank conflicts
     constexpr int HN = BN / 2, XS = HN + 8;
-    constexpr int RB = BM <= 128 ? BM : BM % 128 == 0 ? 128 : 64, NPASS = BM / RB, MTP = RB / 32;
+    constexpr int RB = BM <= 128 ? BM : BM % 128 == 0 ? 128 : BM % 96 == 0 ? 96 : 64, NPASS = BM / RB, MTP = RB / 32;
     // (launched with the 4-bit ring's LDS size at either code width)
     static_assert(2 * RB * XS * 2 <= QmmLds<4, GS, MT, NT, WN, NB>::TOTAL && BM % RB == 0,
                   "gate|up exchange fits the ring");
@@ -723,7 +738,7 @@ __global__ __launch_bounds__(64 * WN * WM) void qmm_kernel(QmmParams p) {
   };
   if constexpr (WM == 1) {
     if (whole && (!p.tiles || MT >= 8) && (p.N & 7) == 0) {
-      // (plain launches and 256-row gather tiles, which runs mostly fill --
+      // (plain launches and 256/288-row gather tiles, which runs mostly fill --
       // a run's short last tile goes to the 64-row kernel: MoE T = 4096
       // 500 -> 478 us; a 128-row gather tile is often a few rows, which the
       // direct stores below serve for less)
