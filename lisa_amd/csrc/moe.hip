@@ -525,6 +525,38 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restric
   const int64_t t = i / H8, d8 = i - t * H8;
   const int TY = k < 8 ? k : 8;
   float total[8];
+  if (k <= 8) {
+    // one slot per partial sum: every slot's index, weight and row piece
+    // loaded before any is used (the loop below would chain k dependent
+    // index-then-row loads), then the same operations in the same order
+    int rows[8];
+    float wr[8];
+    u32x4 v[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      rows[rr] = rr < k ? inv[t * k + rr] : 0;
+      wr[rr] = rr < k ? w[t * k + rr] : 0.0f;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr)
+      if (rr < k) v[rr] = reinterpret_cast<const u32x4*>(down + (int64_t)rows[rr] * H)[d8];
+#pragma unroll
+    for (int y = 0; y < 8; ++y) {
+      if (y >= k) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float a0 = __fadd_rn(__fmul_rn(bf2f_lo(v[y][c]), wr[y]), 0.0f);
+        const float a1 = __fadd_rn(__fmul_rn(bf2f_hi(v[y][c]), wr[y]), 0.0f);
+        total[2 * c] = y == 0 ? a0 : __fadd_rn(a0, total[2 * c]);
+        total[2 * c + 1] = y == 0 ? a1 : __fadd_rn(a1, total[2 * c + 1]);
+      }
+    }
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = pack_bf2(total[2 * c], total[2 * c + 1]);
+    reinterpret_cast<u32x4*>(out + t * H)[d8] = o;
+    return;
+  }
   for (int y = 0; y < TY; ++y) {
     float acc[8];
 #pragma unroll
