@@ -339,7 +339,8 @@ def test_moe_forward_generic_equals_composition(dev, monkeypatch, T, E, k, H, I)
 
 
 @pytest.mark.parametrize("T,E,k,H,I,bits,gs", [(512, 16, 4, 512, 320, 4, 64), (300, 8, 2, 256, 192, 2, 32),
-                                             (1024, 32, 8, 1024, 768, 4, 128), (640, 16, 2, 128, 64, 4, 64)])
+                                             (1024, 32, 8, 1024, 768, 4, 128), (640, 16, 2, 128, 64, 4, 64),
+                                             (1024, 16, 4, 256, 128, 2, 64)])
 def test_gather_qmm_swiglu(dev, oracle, monkeypatch, T, E, k, H, I, bits, gs):
     """The fused gate|up + SwiGLU matmul (x rows read through the sort's row
     map) with skewed routing, so that long runs and a run shorter than the
@@ -350,7 +351,8 @@ def test_gather_qmm_swiglu(dev, oracle, monkeypatch, T, E, k, H, I, bits, gs):
     so the bound is 2e-2 + 2e-2|ref|); and moe_forward, which takes this path
     for T*k >= 20*E, bitwise equal to its steps composed from the public entry
     points (route, sort, gather_qmm_swiglu, gather_qmm(down), combine) and
-    identical in routing to the three-step path (LISAQ_MOE_GU=0)."""
+    identical in routing to the three-step path (LISAQ_MOE_GU=0).  Runs averaging >= 192 rows
+    (T=1024, E=32, k=8 and the 2-bit T=1024, E=16, k=4) take the 288-row tiles."""
     import torch
 
     rng = np.random.default_rng(T + 7 * E + bits)
