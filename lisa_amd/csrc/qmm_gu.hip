@@ -59,11 +59,11 @@ int qmm_gu_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, int 
   LISAQ_REQUIRE((int64_t)p.N * p.K * bits / 8 < ((int64_t)1 << 32), LISAQ_EINVAL_SHAPE,
                 "qmm_gu: one weight matrix larger than 4 GiB");
   LISAQ_REQUIRE(p.N % 8 == 0 && p.K % 64 == 0, LISAQ_EUNSUPPORTED, "qmm_gu: need N %% 8 == 0 and K %% 64 == 0");
-  LISAQ_REQUIRE(rows == 64 || rows == 128 || rows == 256 || rows == 288, LISAQ_EUNSUPPORTED,
-                "qmm_gu: row tile %d not built", rows);
+  LISAQ_REQUIRE(rows == 64 || rows == 128 || rows == kTallBM, LISAQ_EUNSUPPORTED, "qmm_gu: row tile %d not built",
+                rows);
+  static_assert(kTallBM == 288, "tall gate|up tile");
   if (rows == 64) return gu_launch<2, kShortWN>(stream, p, bits, gs, grid);
-  if (rows == 288) return gu_launch<9>(stream, p, bits, gs, grid);
-  return rows == 256 ? gu_launch<8>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
+  return rows == kTallBM ? gu_launch<9>(stream, p, bits, gs, grid) : gu_launch<4>(stream, p, bits, gs, grid);
 }
 
 // Gather launches of 288-row tiles (the MoE prefill's down projection when
@@ -82,11 +82,9 @@ int qmm_gather_launch(hipStream_t stream, const QmmParams& p, int bits, int gs, 
     if (gs == 64) fn = qmm_kernel<B, 64, MT, 1, WN, false, false, NB, kSkip(MT)>;
     if (gs == 128) fn = qmm_kernel<B, 128, MT, 1, WN, false, false, NB, kSkip(MT)>;
   };
-  LISAQ_REQUIRE(rows == 64 || rows == 256 || rows == 288, LISAQ_EUNSUPPORTED, "qmm gather: row tile %d not built",
-                rows);
+  LISAQ_REQUIRE(rows == 64 || rows == kTallBM, LISAQ_EUNSUPPORTED, "qmm gather: row tile %d not built", rows);
   auto pick_mt = [&](auto bt) {
-    if (rows == 288) pick(bt, std::integral_constant<int, 9>{});
-    else if (rows == 256) pick(bt, std::integral_constant<int, 8>{});
+    if (rows == kTallBM) pick(bt, std::integral_constant<int, kTallBM / 32>{});
     else pick(bt, std::integral_constant<int, 2>{});
   };
   if (bits == 4) pick_mt(std::integral_constant<int, 4>{});
