@@ -336,11 +336,13 @@ def config_table(dev, gen, stream):
         qmv_row("north-star shape 4-bit", M, 17408, 5120, 4, 8)
     # [3] 2-bit decode
     qmv_row("decode 2-bit", 1, 17408, 5120, 2, 10)
+    qmv_row("decode 2-bit down", 1, 5120, 17408, 2, 10)
     # [2] prefill: up 17408x5120 and down 5120x17408, M = 128, 512, 2048; [3] 2-bit M = 512
     for M in (128, 512, 2048):
         qmm_row("prefill up 4-bit", M, 17408, 5120, 4)
         qmm_row("prefill down 4-bit", M, 5120, 17408, 4)
     qmm_row("prefill up 2-bit", 512, 17408, 5120, 2)
+    qmm_row("prefill down 2-bit", 512, 5120, 17408, 2)
     rows += moe_rows(dev, gen, stream)
     return rows
 
@@ -416,8 +418,19 @@ def cpu_baseline(M, N, K, bits, gs, seconds):
     c1, e1 = timed(lambda: O.qmv_threads(x, w, s, b, gs, bits, 1), seconds * 0.2)
     xf = O.bf16_to_f32(x)
     cm, em = timed(lambda: xf @ O.dequantize(w, s, b, gs, bits).T, seconds * 0.2, min_calls=2)
+    # the other M = 1 shapes BASELINE names: configs[0] and the configs[1] decode shapes (same threads)
+    shapes = []
+    for name, n_, k_ in (("configs[0] 3072x1024", 3072, 1024), ("configs[1] up 9728x2560", 9728, 2560),
+                         ("configs[1] down 2560x9728", 2560, 9728)):
+        w2, s2, b2 = np_linear(rng, n_, k_, 4, gs, s_floor=1e-3 if n_ == 3072 else 0.0)
+        x2 = np_x(rng, 1, k_)
+        nb2 = qmv_bytes(1, n_, k_, 4, gs)
+        c2, e2 = timed(lambda: O.qmv_threads(x2, w2, s2, b2, gs, 4, threads), max(seconds * 0.1, 0.5), min_calls=3)
+        shapes.append({"workload": name, "N": n_, "K": k_, "bits": 4, "M": 1, "cores": threads, "calls": c2,
+                       "us_per_call": round(e2 / c2 * 1e6, 1), "value": round(nb2 * c2 / e2 / 1e9, 3), "unit": "GB/s"})
     return {
         "value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "configs": shapes,
         "host_cpus": host_cpus, "single_thread_value": round(nbytes * c1 / e1 / 1e9, 3),
         "sample": f"{calls} calls of the same qmv shape (M={M} K={K} N={N} {bits}-bit) in {el:.1f} s on {threads} "
                   f"threads; 1 thread: {nbytes * c1 / e1 / 1e9:.3f} GB/s ({c1} calls); dequantize-then-matmul: "

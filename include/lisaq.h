@@ -57,6 +57,18 @@ LISAQ_API int lisaq_version(void);
 /* Message for the last failing call on this thread ("" if none). */
 LISAQ_API const char* lisaq_last_error(void);
 
+/* Test/diagnostic path selection.  No counterpart in the reference: it lets
+ * parity tests force each kernel the dispatcher can pick (every one is valid
+ * for the shapes it accepts).  Names: LISAQ_QMV_KERNEL (value = the kernel's
+ * letter 'w','p','d','t','1' (16-row),'3' (32-row); a shape the kernel does
+ * not take falls through to the next), LISAQ_QMM_SPLIT (matmul parts over K),
+ * LISAQ_GATHER_SHORT, LISAQ_MOE_GU, LISAQ_MOE_FUSED, LISAQ_MOE_GU_MV (0 = off).
+ * LISAQ_PATH_DEFAULT restores the dispatcher's choice.  Process-wide, read by
+ * every later dispatch; never read from the environment.  Unknown name:
+ * LISAQ_EINVAL_SHAPE. */
+#define LISAQ_PATH_DEFAULT (-2147483647 - 1)
+LISAQ_API int lisaq_set_path_override(const char* name, int value);
+
 /* ---- quantized matmul ---------------------------------------------------
  * y[M,N] (bf16) = x[M,K] (bf16) . dequant(w)^T.
  * Replaces ops::quantized_matmul (AO:378-493).  transpose must be 1 and

@@ -43,6 +43,7 @@ cip = ctypes.POINTER(ctypes.c_int)
 SIGNATURES = {
     "lisaq_version": (ci, []),
     "lisaq_last_error": (ctypes.c_char_p, []),
+    "lisaq_set_path_override": (ci, [ctypes.c_char_p, ci]),
     "lisaq_quantized_matmul": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci, vp, sz]),
     "lisaq_quantized_matmul_workspace": (sz, [i64, i64, i64, ci, ci]),
     "lisaq_quantized_matmul_noalloc": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci]),
@@ -101,3 +102,19 @@ def check(rc: int) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args))
+
+
+PATH_DEFAULT = -(2**31)
+
+
+def set_path_override(name: str, value) -> None:
+    """Force a dispatch path (test/diagnostic; see lisaq_set_path_override).
+    ``value``: an int, a kernel letter string (first character used) or None
+    for the dispatcher's own choice."""
+    if value is None:
+        v = PATH_DEFAULT
+    elif isinstance(value, str):
+        v = int(value) if value.lstrip("-").isdigit() and name != "LISAQ_QMV_KERNEL" else ord(value[0])
+    else:
+        v = int(value)
+    check(load().lisaq_set_path_override(name.encode(), v))

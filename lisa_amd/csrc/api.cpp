@@ -8,6 +8,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
+#include <climits>
 #include <mutex>
 #include <vector>
 
@@ -38,15 +40,29 @@ int tune_int(const char* name, int dflt) {
   return dflt;
 }
 
-int path_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : dflt;
+// Path overrides: set only through lisaq_set_path_override (never read from
+// the environment), so a serving process runs the dispatcher's choice unless
+// its own code asks otherwise.  kPathNone = unset.
+static const char* const kPathNames[] = {"LISAQ_QMV_KERNEL", "LISAQ_QMM_SPLIT", "LISAQ_GATHER_SHORT",
+                                         "LISAQ_MOE_GU", "LISAQ_MOE_FUSED", "LISAQ_MOE_GU_MV"};
+static constexpr int kPathNone = INT32_MIN;
+static constexpr int kNumPaths = (int)(sizeof(kPathNames) / sizeof(kPathNames[0]));
+static std::atomic<int> g_path[kNumPaths] = {{kPathNone}, {kPathNone}, {kPathNone},
+                                             {kPathNone}, {kPathNone}, {kPathNone}};
+
+static int path_slot(const char* name) {
+  for (int i = 0; i < kNumPaths; ++i)
+    if (name && strcmp(name, kPathNames[i]) == 0) return i;
+  return -1;
 }
 
-char path_char(const char* name) {
-  const char* v = getenv(name);
-  return v ? v[0] : 0;
+int path_int(const char* name, int dflt) {
+  const int i = path_slot(name);
+  const int v = i < 0 ? kPathNone : g_path[i].load(std::memory_order_relaxed);
+  return v == kPathNone ? dflt : v;
 }
+
+char path_char(const char* name) { return (char)path_int(name, 0); }
 
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
@@ -448,6 +464,13 @@ using namespace lisaq;
 extern "C" {
 
 int lisaq_version(void) { return 100; }
+
+int lisaq_set_path_override(const char* name, int value) {
+  const int i = lisaq::path_slot(name);
+  LISAQ_REQUIRE(i >= 0, LISAQ_EINVAL_SHAPE, "set_path_override: unknown path %s", name ? name : "(null)");
+  lisaq::g_path[i].store(value == LISAQ_PATH_DEFAULT ? lisaq::kPathNone : value, std::memory_order_relaxed);
+  return LISAQ_OK;
+}
 
 const char* lisaq_last_error(void) { return g_err; }
 

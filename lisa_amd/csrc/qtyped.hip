@@ -193,6 +193,9 @@ int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* 
                     void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype) {
   const typed_fn fn = matvec ? pick<true>(dtype, bits, gs) : pick<false>(dtype, bits, gs);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "quantized_matmul_typed: dtype=%d bits=%d gs=%d", dtype, bits, gs);
+  // grid.y carries the 64-row tiles of M (at most 65535 of them)
+  if (!matvec && (M + 63) / 64 > 65535)
+    return set_error(LISAQ_EINVAL_SHAPE, "quantized_matmul_typed: M=%lld exceeds %d rows", (long long)M, 65535 * 64);
   if (matvec)
     hipLaunchKernelGGL(fn, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, w, s, b, y, (int)M, (int)N, (int)K);
   else

@@ -42,3 +42,20 @@ def oracle():
     return O
 
 
+
+
+@pytest.fixture
+def force_path():
+    """force_path(name, value): select a dispatch path through the library's
+    explicit override entry point for the duration of one test."""
+    from lisa_amd import _lib
+
+    used = set()
+
+    def set_(name, value):
+        used.add(name)
+        _lib.set_path_override(name, value)
+
+    yield set_
+    for name in used:
+        _lib.set_path_override(name, None)

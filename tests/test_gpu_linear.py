@@ -75,10 +75,10 @@ def test_qmv_parity(dev, oracle, M, N, K, bits, gs):
     (2, 4097, 2560, 4, 32),     # four rows a step (K = 2560), ragged last step, two rows of x
     (1, 1001, 5120, 4, 128),    # two rows a step (K = 5120), odd N
 ])
-def test_qmv_every_kernel(dev, oracle, monkeypatch, kernel, M, N, K, bits, gs):
+def test_qmv_every_kernel(dev, oracle, force_path, kernel, M, N, K, bits, gs):
     """Each matvec kernel (forced through LISAQ_QMV_KERNEL; a shape it does not
     take falls through to the next one) against the oracle."""
-    monkeypatch.setenv("LISAQ_QMV_KERNEL", kernel)
+    force_path("LISAQ_QMV_KERNEL", kernel)
     rng = np.random.default_rng(N * 3 + K + bits + gs + M)
     w, s, b = np_linear(rng, N, K, bits, gs, s_std=0.02 if bits == 4 else 0.05,
                         b_std=0.01 if bits == 4 else 0.02)
@@ -105,10 +105,10 @@ def test_qmm_parity(dev, oracle, M, N, K, bits, gs):
 
 
 @pytest.mark.parametrize("split", ["1", "2", "3", "7"])
-def test_qmm_split_k(dev, oracle, monkeypatch, split):
+def test_qmm_split_k(dev, oracle, force_path, split):
     """The matmul split over K (f32 partials in the workspace, summed in split
     order): every split count against the oracle, and the same bits on a repeat."""
-    monkeypatch.setenv("LISAQ_QMM_SPLIT", split)
+    force_path("LISAQ_QMM_SPLIT", split)
     rng = np.random.default_rng(77)
     M, N, K = 70, 300, 1024
     w, s, b = np_linear(rng, N, K, 4, 64)
@@ -121,7 +121,7 @@ def test_qmm_split_k(dev, oracle, monkeypatch, split):
 
 @pytest.mark.parametrize("M,N,K,bits", [(128, 17408, 5120, 4), (128, 5120, 17408, 4), (512, 17408, 5120, 4),
                                         (512, 5120, 17408, 4), (2048, 17408, 5120, 4), (2048, 5120, 17408, 4),
-                                        (512, 17408, 5120, 2)])
+                                        (512, 17408, 5120, 2), (512, 5120, 17408, 2)])
 def test_qmm_prefill_shapes_sampled_rows(dev, oracle, M, N, K, bits):
     """configs[2]/[3] prefill shapes; the oracle checks 8 sampled rows (every column)."""
     import torch
@@ -140,12 +140,12 @@ def test_qmm_prefill_shapes_sampled_rows(dev, oracle, M, N, K, bits):
 
 
 @pytest.mark.parametrize("M", [4, 8])
-def test_qmv_split_k_and_its_fallback(dev, oracle, monkeypatch, M):
+def test_qmv_split_k_and_its_fallback(dev, oracle, force_path, M):
     """Few row tiles (N = 2560): the streaming matvec splits K over workgroups when the workspace holds
     the parts; given none, the same call runs unsplit. Both against the oracle, and close to each other."""
     import torch
 
-    monkeypatch.setenv("LISAQ_QMV_KERNEL", "t")
+    force_path("LISAQ_QMV_KERNEL", "t")
 
     from lisa_amd import _lib
 
@@ -191,14 +191,28 @@ def test_north_star_qmv_shape(dev, oracle, bits):
         assert np.array_equal(_run(ops.quantized_matmul, dev, x, w, s, b, 64, bits), got)
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+def test_down_shape_qmv(dev, oracle, bits):
+    """configs[3] (2-bit) and configs[2] (4-bit) down shape at decode: N = 5120, K = 17408 (272 groups a
+    row), M = 1 over every row, with the config's scale/bias distributions."""
+    rng = np.random.default_rng(5120 + bits)
+    N, K = 5120, 17408
+    w, s, b = np_linear(rng, N, K, bits, 64, s_std=0.02 if bits == 4 else 0.05, b_std=0.01 if bits == 4 else 0.02)
+    for M in (1, 4):
+        x = np_x(rng, M, K)
+        ref = oracle.qmv(x, w, s, b, 64, bits)
+        got = _run(ops.quantized_matmul, dev, x, w, s, b, 64, bits)
+        assert_close_bf16(got, ref, what=f"down-shape qmv M={M} bits={bits}")
+
+
 @pytest.mark.parametrize("N,K,gs", [(17408, 5120, 64), (9728, 2560, 64), (2560, 9728, 64), (1000, 1024, 64),
                                     (777, 2048, 128), (5, 512, 64)])
-def test_one_stream_rows_bitwise(dev, oracle, monkeypatch, N, K, gs):
+def test_one_stream_rows_bitwise(dev, oracle, force_path, N, K, gs):
     """The one-stream matvec (1..8 rows of x on one pass over W): every row of an M-row call is bitwise
     equal to the same kernel's one-row call (the matrix-core column of a row never mixes other rows), for
     every M; every row within tolerance of the oracle.  Eight rows at K = 9728 stage x in two passes over
     K (all of it does not fit the LDS): bitwise equal to the one-pass one-row call as well."""
-    monkeypatch.setenv("LISAQ_QMV_KERNEL", "w")
+    force_path("LISAQ_QMV_KERNEL", "w")
     rng = np.random.default_rng(N + K + gs)
     w, s, b = np_linear(rng, N, K, 4, gs)
     x = np_x(rng, 8, K)

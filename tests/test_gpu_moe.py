@@ -118,10 +118,10 @@ def test_gather_qmm_parity(dev, oracle, R, E, N, K):
 
 @pytest.mark.parametrize("kernel", ["d", "t"])
 @pytest.mark.parametrize("R,E,N,K", [(1, 4, 768, 2048), (2, 4, 768, 2048), (2, 2, 2048, 768), (2, 1, 300, 512)])
-def test_gather_qmm_short_runs(dev, oracle, monkeypatch, kernel, R, E, N, K):
+def test_gather_qmm_short_runs(dev, oracle, force_path, kernel, R, E, N, K):
     """Runs of one or two rows (decode MoE) through each tile-capable matvec
     kernel (forced with LISAQ_QMV_KERNEL)."""
-    monkeypatch.setenv("LISAQ_QMV_KERNEL", kernel)
+    force_path("LISAQ_QMV_KERNEL", kernel)
     rng = np.random.default_rng(R * 11 + E + N)
     W, S, B = _expert_stack(rng, E, N, K)
     ids = np.sort(rng.integers(0, E, R)).astype(np.int32)
@@ -133,12 +133,12 @@ def test_gather_qmm_short_runs(dev, oracle, monkeypatch, kernel, R, E, N, K):
 
 
 @pytest.mark.parametrize("kernel", [None, "t"])
-def test_gather_qmm_walking_grid(dev, oracle, monkeypatch, kernel):
+def test_gather_qmm_walking_grid(dev, oracle, force_path, kernel):
     """Long runs with a dozen short ones among them: R >= 4 x the matvec limit x E, so the matvec's
     tile-table launch is a short grid whose blocks walk the table (1,536 matvec tiles over 1,024
     blocks: some blocks take two)."""
     if kernel:
-        monkeypatch.setenv("LISAQ_QMV_KERNEL", kernel)
+        force_path("LISAQ_QMV_KERNEL", kernel)
     E, N, K = 16, 2048, 512
     limit = ops.qmv_batch_limit(K, N)
     rng = np.random.default_rng(2024)
@@ -206,7 +206,7 @@ def test_moe_forward_parity(dev, oracle, T):
                                                     (40, 16, 2, 512, 320, 2, 64, True),
                                                     (9, 8, 3, 256, 256, 4, 128, False),
                                                     (24, 16, 4, 256, 192, 4, 32, True)])
-def test_moe_forward_gate_up_matvec(dev, monkeypatch, T, E, k, H, I, bits, gs, skew):
+def test_moe_forward_gate_up_matvec(dev, force_path, T, E, k, H, I, bits, gs, skew):
     """Between the decode window and the gate|up matmul path (9 <= T, T*k < 20E): gate|up + SwiGLU in
     the gate|up streaming matvec (and the gate|up matmul for runs at or above the matvec limit; skewed
     routing makes such runs), x read through the row map -- bitwise equal to the same block with gate,
@@ -223,7 +223,7 @@ def test_moe_forward_gate_up_matvec(dev, monkeypatch, T, E, k, H, I, bits, gs, s
     dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(s_)) for s_ in (G, U, D)]
     xd, lgd = to_dev_bf16(x, dev), to_dev(lg, dev)
     fused = from_dev_bf16(ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, group_size=gs, bits=bits))
-    monkeypatch.setenv("LISAQ_MOE_GU_MV", "0")
+    force_path("LISAQ_MOE_GU_MV", "0")
     steps = from_dev_bf16(ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, group_size=gs, bits=bits))
     torch.cuda.synchronize()
     assert np.array_equal(fused, steps)
@@ -283,7 +283,7 @@ def test_moe_forward_baseline_shape(dev, oracle):
 @pytest.mark.parametrize("T,E,k,H,I,bits,gs", [(1, 128, 8, 2048, 768, 4, 64), (3, 16, 4, 512, 256, 4, 32),
                                              (8, 32, 2, 1024, 384, 4, 128), (2, 64, 8, 256, 768, 2, 64),
                                              (5, 32, 16, 128, 1024, 2, 128), (1, 4, 1, 4096, 64, 4, 64)])
-def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
+def test_moe_fused_decode_vs_generic(dev, force_path, T, E, k, H, I, bits, gs):
     """The fused decode path (T <= 8: gate|up+SwiGLU and down+combine kernels)
     against the generic path (sort, gather_qmm, SwiGLU, combine) on the same
     inputs: identical routing, outputs within the output tolerance (the two
@@ -299,7 +299,7 @@ def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
     assert _lib.load().lisaq_moe_decode_supported(T, H, I, E, k, gs, bits) == 1
     outs = {}
     for fused in ("1", "0"):
-        monkeypatch.setenv("LISAQ_MOE_FUSED", fused)
+        force_path("LISAQ_MOE_FUSED", fused)
         o, idx, w = ops.moe_forward(to_dev_bf16(x, dev), to_dev(lg, dev), dv[0], dv[1], dv[2], k, gs, bits,
                                     return_routing=True)
         outs[fused] = (from_dev_bf16(o), idx.cpu().numpy(), w.cpu().numpy())
@@ -311,7 +311,7 @@ def test_moe_fused_decode_vs_generic(dev, monkeypatch, T, E, k, H, I, bits, gs):
 
 @pytest.mark.parametrize("T,E,k,H,I", [(600, 64, 8, 128, 64), (300, 1024, 4, 256, 128), (600, 1023, 2, 256, 128),
                                        (2100, 1024, 4, 256, 128)])
-def test_moe_forward_generic_equals_composition(dev, monkeypatch, T, E, k, H, I):
+def test_moe_forward_generic_equals_composition(dev, force_path, T, E, k, H, I):
     """moe_forward's generic path (multi-workgroup counting sort, tile tables
     built from the expert offsets) against the same steps composed from the
     public entry points (one-workgroup sort, tile tables from the sorted ids):
@@ -320,7 +320,7 @@ def test_moe_forward_generic_equals_composition(dev, monkeypatch, T, E, k, H, I)
     with one thread per expert row, and with a wave per row at 17 blocks)."""
     import torch
 
-    monkeypatch.setenv("LISAQ_MOE_FUSED", "0")
+    force_path("LISAQ_MOE_FUSED", "0")
     rng = np.random.default_rng(T + E)
     G, U, D = _expert_stack(rng, E, I, H), _expert_stack(rng, E, I, H), _expert_stack(rng, E, H, I)
     x = to_dev_bf16(np_x(rng, T, H), dev)
@@ -338,10 +338,43 @@ def test_moe_forward_generic_equals_composition(dev, monkeypatch, T, E, k, H, I)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
+@pytest.mark.parametrize("I", [200, 72])
+def test_gather_qmm_swiglu_partial_column_block(dev, oracle, I):
+    """I not a multiple of 64: the gate|up tile's last 64-column block ends
+    partway (the epilogue's column clamp and its gate/up exchange on a partial
+    block).  Every run against the oracle's matmul arithmetic (gate and up
+    rounded to bf16, then the bf16 SwiGLU: bound 2e-2 + 2e-2|ref|)."""
+    import torch
+
+    T, E, k, H, gs, bits = 256, 8, 2, 256, 64, 4
+    rng = np.random.default_rng(I)
+    stk = lambda n, kk: tuple(a.reshape(E, n, -1) for a in np_linear(rng, E * n, kk, bits, gs))
+    G, U = stk(I, H), stk(I, H)
+    x = np_x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U)]
+    xd = to_dev_bf16(x, dev)
+    ridx, _ = ops.moe_route(to_dev(lg, dev), k)
+    srt, order, rows, inv, offs = ops.moe_sort(ridx.reshape(-1), E, k)
+    act = from_dev_bf16(ops.gather_qmm_swiglu(xd, rows, dv[0], dv[1], srt, gs, bits))
+    torch.cuda.synchronize()
+    offs_h, rows_h = offs.cpu().numpy(), rows.cpu().numpy()
+    assert act.shape == (T * k, I)
+    for e in range(E):
+        a, b = offs_h[e], offs_h[e + 1]
+        if b == a:
+            continue
+        xr = x[rows_h[a:b]]
+        g = oracle.f32_to_bf16(oracle.qmm(xr, G[0][e], G[1][e], G[2][e], gs, bits))
+        u = oracle.f32_to_bf16(oracle.qmm(xr, U[0][e], U[1][e], U[2][e], gs, bits))
+        ref = bf16_bits_to_f32(oracle.swiglu(g, u))
+        assert_close_bf16(act[a:b], ref, rtol=2e-2, what=f"I={I} expert {e} ({b - a} rows)")
+
+
 @pytest.mark.parametrize("T,E,k,H,I,bits,gs", [(512, 16, 4, 512, 320, 4, 64), (300, 8, 2, 256, 192, 2, 32),
                                              (1024, 32, 8, 1024, 768, 4, 128), (640, 16, 2, 128, 64, 4, 64),
                                              (1024, 16, 4, 256, 128, 2, 64)])
-def test_gather_qmm_swiglu(dev, oracle, monkeypatch, T, E, k, H, I, bits, gs):
+def test_gather_qmm_swiglu(dev, oracle, force_path, T, E, k, H, I, bits, gs):
     """The fused gate|up + SwiGLU matmul (x rows read through the sort's row
     map) with skewed routing, so that long runs and a run shorter than the
     matvec limit (5 rows) occur: runs at or above the limit bitwise equal to
@@ -391,7 +424,7 @@ def test_gather_qmm_swiglu(dev, oracle, monkeypatch, T, E, k, H, I, bits, gs):
     d = ops.gather_qmm(act, *dv[2], rhs_indices=srt, group_size=gs, bits=bits)
     ref = ops.moe_combine(d, rw.reshape(-1), inv, T, k)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
-    monkeypatch.setenv("LISAQ_MOE_GU", "0")
+    force_path("LISAQ_MOE_GU", "0")
     out0, idx0, w0 = ops.moe_forward(xd, lgd, dv[0], dv[1], dv[2], k, gs, bits, return_routing=True)
     assert torch.equal(idx, idx0) and torch.equal(w, w0)
     long_tok = np.all(sizes[idx.cpu().numpy()] >= lim, axis=1)
@@ -402,7 +435,7 @@ def test_gather_qmm_swiglu(dev, oracle, monkeypatch, T, E, k, H, I, bits, gs):
 
 @pytest.mark.parametrize("runs", [(300, 64, 65, 256, 320, 1, 40, 129, 0, 513),
                                   (200, 33, 100, 64, 128, 190, 16, 255)])
-def test_gather_short_last_tiles(dev, oracle, monkeypatch, runs):
+def test_gather_short_last_tiles(dev, oracle, force_path, runs):
     """A run's last matmul tile of at most 64 rows goes to the short-tile kernel: gather_qmm and
     gather_qmm_swiglu bitwise equal to the same calls with every tile in the tall kernel
     (LISAQ_GATHER_SHORT=0), and gather_qmm's runs against the per-run oracle."""
@@ -429,7 +462,7 @@ def test_gather_short_last_tiles(dev, oracle, monkeypatch, runs):
         return y, a
 
     y, a = both()
-    monkeypatch.setenv("LISAQ_GATHER_SHORT", "0")
+    force_path("LISAQ_GATHER_SHORT", "0")
     y0, a0 = both()
     assert np.array_equal(y, y0)
     assert np.array_equal(a, a0)

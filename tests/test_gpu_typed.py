@@ -71,3 +71,29 @@ def test_promotion_bf16_x_f32_scales(dev, oracle):
                              _tensor(bf, "f32", dev), True, gs, bits)
     assert y.dtype == torch.float32
     _close(y.cpu().numpy(), oracle.qmv_typed(x, w, sf, bf, gs, bits), "f32", "promoted")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("M", [1, 64])
+def test_quantized_matmul_typed_long_k(dev, oracle, dtype, M):
+    """K = 5120: the matvec's lanes take several 32-code chunks each (K/32 =
+    160 chunks over 64 lanes) and the matmul's K loop runs 80 steps over 16
+    column tiles."""
+    import torch
+
+    rng = np.random.default_rng(5120 + M)
+    N, K, gs, bits = 1000, 5120, 64, 4
+    w, s, b = np_linear(rng, N, K, bits, gs)
+    sf = oracle._round_to(bf16_bits_to_f32(s), dtype)
+    bf = oracle._round_to(bf16_bits_to_f32(b), dtype)
+    xf = oracle._round_to(rng.standard_normal((M, K)).astype(np.float32), dtype)
+    y = ops.quantized_matmul(_tensor(xf, dtype, dev), to_dev_u32(w, dev), _tensor(sf, dtype, dev),
+                             _tensor(bf, dtype, dev), True, gs, bits)
+    got = y.float().cpu().numpy()
+    assert (M < ops.qmv_batch_limit(K, N)) == (M == 1)  # both sides of the split
+    if M == 1:
+        ref = oracle.qmv_typed(xf, w, sf, bf, gs, bits)
+    else:
+        ref = oracle.qmm_typed(xf, w, sf, bf, gs, bits, dtype)
+    _close(got, ref, dtype, f"{dtype} K={K} M={M}")
+    torch.cuda.synchronize()
