@@ -128,7 +128,7 @@ static int run_qmv(hipStream_t st, const QmvConfig& c, const void* x, const uint
   // parts it runs unsplit
   if (c.kind == 2 && c.S > 1 && (ws == nullptr || ws_bytes < c.ws_bytes || !aligned(ws, 256)))
     return run_qmv(st, qmv_config(M, N, K, gs, bits, true), x, w, s, b, y, M, N, K, gs, bits, nullptr, 0);
-  if (c.S > 1) {
+  if (c.ws_bytes > 0) {  // (c.S is the ring depth or the workgroup count for the other kinds)
     LISAQ_REQUIRE(ws != nullptr && ws_bytes >= c.ws_bytes, LISAQ_EWORKSPACE,
                   "qmv: workspace of %zu bytes required (got %zu)", c.ws_bytes, ws_bytes);
     LISAQ_REQUIRE(aligned(ws, 256), LISAQ_EINVAL_LAYOUT, "qmv: workspace must be 256-byte aligned");
@@ -646,6 +646,28 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
     }
     return LISAQ_OK;
   }
+  if (c.kind == 6) {
+    // the wave-rows kernel's arithmetic is the persistent kernel's: pairs of
+    // rows share one pass over W (in either kernel); rows one at a time where
+    // no two-row configuration exists (long rows)
+    for (int64_t r = 0; r < M; r += 2) {
+      const int64_t mr = M - r < 2 ? M - r : 2;
+      QmvConfig cp = mr == 1 ? c : qmvs_config(2, N, K, gs, bits);
+      if (cp.kind != 6 && mr == 2) cp = qmvp_config(2, N, K, gs, bits);
+      if (cp.kind != 6 && cp.kind != 4) {
+        for (int64_t q = r; q < r + mr; ++q) {
+          rc = run_qmv((hipStream_t)stream, c, (const uint16_t*)x + q * K, w, s, b, (uint16_t*)y + q * N, 1, N, K,
+                       gs, bits, ws, ws_bytes);
+          if (rc) return rc;
+        }
+        continue;
+      }
+      rc = run_qmv((hipStream_t)stream, cp, (const uint16_t*)x + r * K, w, s, b, (uint16_t*)y + r * N, mr, N, K,
+                   gs, bits, ws, ws_bytes);
+      if (rc) return rc;
+    }
+    return LISAQ_OK;
+  }
   if (c.kind == 3) {
     // the dot kernel computes every row of a launch with the same arithmetic
     // (any MR), so pairs of rows share one pass over W
@@ -729,6 +751,28 @@ int lisaq_qmv_addnorm(void* stream, const void* x, const void* r, const void* no
     p.norm_out = (uint16_t*)norm_out;
     p.eps = eps;
     return qmvp_addnorm_launch(st, c, p, bits, gs);
+  }
+  if (c.kind == 6) {
+    // the wave-rows matvec with the add + RMSNorm prologue in every workgroup: one launch
+    const QmvConfig ca = qmvs_config(1, N, K, gs, bits, true);
+    if (ca.kind == 6) {
+      QmvParams p{};
+      p.x = (const uint16_t*)x;
+      p.w = w;
+      p.s = (const uint16_t*)s;
+      p.b = (const uint16_t*)b;
+      p.y = (uint16_t*)y;
+      p.M = 1;
+      p.N = (int)N;
+      p.K = (int)K;
+      p.G = (int)(K / gs);
+      p.r = (const uint16_t*)r;
+      p.nw = (const uint16_t*)norm_w;
+      p.sum_out = (uint16_t*)sum_out;
+      p.norm_out = (uint16_t*)norm_out;
+      p.eps = eps;
+      return qmvs_addnorm_launch(st, ca, p, bits, gs);
+    }
   }
   if (int rc = launch_add_rms(st, (const uint16_t*)x, (const uint16_t*)r, (const uint16_t*)norm_w,
                               (uint16_t*)sum_out, (uint16_t*)norm_out, M, K, eps))

@@ -51,7 +51,8 @@ struct QmvConfig {
                   // 3: VALU dot kernel (U = rows per thread, S = rows side by side, S_inner = chunks),
                   // 4: persistent one-row dot kernel (U = passes, S = ring depth, S_inner = chunks),
                   // 5: one-stream 1..8-row MFMA kernel (MR = staged rows, S = workgroups, U = ring units,
-                  //    tile_rows = 16-row tiles per workgroup at most)
+                  //    tile_rows = 16-row tiles per workgroup at most),
+                  // 6: one or two rows, a wave per block of rows (U = passes, S = rows per wave)
   int tile_rows;  // rows of W per workgroup (32 or 16)
   int U, MQ, NW, S, S_inner, slab_groups, tiles, lds_bytes;
   int tpb;  // streaming kernel: 16-row tiles per block (0 or 1: one)
@@ -98,6 +99,12 @@ int qmvp_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
 // the persistent kernel with the residual add + RMSNorm prologue (p.r, p.nw,
 // p.sum_out, p.norm_out, p.eps set; one row; c from qmvp_config(1, ...))
 int qmvp_addnorm_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs);
+
+// one or two rows, a wave per block of rows, every load of the matrix issued
+// at once (the one-row kernel's arithmetic; plain rows only, gs 64)
+QmvConfig qmvs_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool addnorm = false);
+int qmvs_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs);
+int qmvs_addnorm_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs);
 
 // Enqueue; grid_x = number of row tiles (or tile-table entries).
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);

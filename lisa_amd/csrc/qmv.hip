@@ -428,7 +428,7 @@ QmvConfig qmv32_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
 // agent-scope release/acquire, which on a multi-XCD MI355X writes back and
 // invalidates L2 and measured 3x slower than one pass per row tile.)
 QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool single_pass) {
-  // path selection: "w" one-stream rows, "p" persistent, "d" dot, "t"
+  // path selection: "w" one-stream rows, "p" persistent, "s" wave-rows, "d" dot, "t"
   // streaming, "1" 16-row, "3" 32-row (a kernel that refuses the shape falls
   // through to the next in this order)
   const char f = path_char("LISAQ_QMV_KERNEL");
@@ -437,6 +437,10 @@ QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool sin
     if (!single_pass && (f == 'w' || f == 'p') && M <= 2) {
       const QmvConfig c = qmvp_config(M, N, K, gs, bits);
       if (c.kind == 4) return c;
+    }
+    if (!single_pass && (f == 'w' || f == 'p' || f == 's') && M <= 2) {
+      const QmvConfig c = qmvs_config(M, N, K, gs, bits);
+      if (c.kind == 6) return c;
     }
     if ((f == 'w' || f == 'p' || f == 'd') && qmvd_supported(M, N, K, gs, bits)) return qmvd_config(M, N, K, gs, bits);
     if (f != '1' && f != '3' && qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits, !single_pass);
@@ -452,6 +456,12 @@ QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool sin
     const QmvConfig c = qmvp_config(M, N, K, gs, bits);
     if (c.kind == 4) return c;
   }
+  if (!single_pass && M == 1) {
+    // measured (cold, graph-replayed) against the dot kernel below: 9728 x 2560
+    // 5.6 vs 6.2 us, 2560 x 9728 5.9 vs 7.7, 5120 x 17408 13.8 vs 19.2 (2-bit 14.1 vs 16.5)
+    const QmvConfig c = qmvs_config(M, N, K, gs, bits);
+    if (c.kind == 6) return c;
+  }
   if (M == 1 && qmvd_supported(M, N, K, gs, bits)) return qmvd_config(M, N, K, gs, bits);
   if (qmvt_supported(M, K, gs, bits)) return qmvt_config(M, N, K, gs, bits, !single_pass);
   if (qmv16_supported(M, gs, bits)) return qmv16_config(M, N, K, gs, bits);
@@ -459,6 +469,7 @@ QmvConfig qmv_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool sin
 }
 
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x) {
+  if (c.kind == 6) return qmvs_launch(stream, c, p, bits, gs);
   if (c.kind == 5) return qmvw_launch(stream, c, p, bits, gs, grid_x);
   if (c.kind == 4) return qmvp_launch(stream, c, p, bits, gs, grid_x);
   if (c.kind == 3) return qmvd_launch(stream, c, p, bits, gs, grid_x);
@@ -467,7 +478,7 @@ int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, in
 }
 
 int qmv_lds_bytes_for(const QmvConfig& c, int gs, int M, int bits) {
-  if (c.kind == 5 || c.kind == 4) return c.lds_bytes;
+  if (c.kind == 6 || c.kind == 5 || c.kind == 4) return c.lds_bytes;
   if (c.kind == 3) return qmvd_lds_bytes(c, M);
   if (c.kind == 2) return qmvt_lds_bytes(c, gs, M, bits);
   return c.kind == 1 ? qmv16_lds_bytes(c.slab_groups, gs, M, c.MQ, bits, c.NW)

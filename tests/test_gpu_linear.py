@@ -61,7 +61,7 @@ def test_qmv_parity(dev, oracle, M, N, K, bits, gs):
         assert np.array_equal(got, got2)
 
 
-@pytest.mark.parametrize("kernel", ["w", "p", "d", "t", "16", "32"])
+@pytest.mark.parametrize("kernel", ["w", "p", "s", "d", "t", "16", "32"])
 @pytest.mark.parametrize("M,N,K,bits,gs", [
     (1, 100, 1024, 4, 64),      # fewer rows than waves (persistent kernel), J = 1
     (1, 4099, 2560, 4, 64),     # J = 2, N tail
@@ -245,7 +245,7 @@ def _one_stream_fits(M, N, K):
 def test_serial_rows_bitwise_equal_to_single_rows(dev, bits):
     """array_ops.rs:650-710: batched rows == independent M=1 calls, bitwise."""
     rng = np.random.default_rng(99 + bits)
-    for N, K in ((64, 512), (2560, 9728), (9728, 2560), (17408, 5120)):
+    for N, K in ((64, 512), (2560, 9728), (9728, 2560), (17408, 5120), (1000, 17408)):
         w, s, b = np_linear(rng, N, K, bits, 64)
         x = np_x(rng, 3, K)
         batched = _run(ops.quantized_matmul_serial_rows, dev, x, w, s, b, 64, bits)
@@ -328,13 +328,13 @@ def test_rejections_raise(dev):
                              to_dev_bf16(s, dev), to_dev_bf16(b, dev))
 
 
-@pytest.mark.parametrize("N,K", [(264, 5120), (1000, 9728), (17408, 5120), (16384, 4608)])
+@pytest.mark.parametrize("N,K", [(264, 5120), (1000, 9728), (17408, 5120), (16384, 4608), (5120, 5120)])
 def test_qmv_addnorm(dev, oracle, N, K):
     """Residual add + RMSNorm + matvec (jit::affine_qmv_fast_addnorm, matmul.rs:315-443): the sum row
     bit-exact; the normed row within one bf16 step of the oracle (the f32 sum of squares may differ in
     its last bit from the float64 one); y bitwise equal to the matvec on the kernel's own normed row and
-    within tolerance of the oracle's matvec on the oracle's normed row.  N >= 16384 with K <= 6144 takes the
-    persistent matvec with the add + RMSNorm folded in (one launch); the other shapes the two-launch path."""
+    within tolerance of the oracle's matvec on the oracle's normed row.  Every shape here is one launch: the
+    persistent matvec (N >= 16384, K <= 6144) or the wave-rows matvec, each with the add + RMSNorm folded in."""
     import torch
 
     rng = np.random.default_rng(N + K)
@@ -359,3 +359,65 @@ def test_qmv_addnorm(dev, oracle, N, K):
     _, _, none = ops.qmv_addnorm(to_dev_bf16(x, dev), to_dev_bf16(r, dev), to_dev_bf16(nw, dev), *dw, 1e-6,
                                  write_norm=False)
     assert none is None
+
+
+@pytest.mark.parametrize("M,N,K,bits", [(1, 17408, 5120, 4), (2, 17408, 5120, 4), (1, 9728, 2560, 4), (1, 2560, 9728, 4),
+                                        (8, 2560, 9728, 4), (1, 17408, 5120, 2)])
+def test_null_workspace_when_none_needed(dev, M, N, K, bits):
+    """A caller that passes NULL/0 where lisaq_quantized_matmul_workspace() is 0 gets the same bits as
+    one that passes a workspace (the header's contract)."""
+    import torch
+
+    from lisa_amd import _lib
+
+    lib = _lib.load()
+    if lib.lisaq_quantized_matmul_workspace(M, N, K, 64, bits) != 0:
+        pytest.skip("this shape uses a workspace")
+    rng = np.random.default_rng(N + K + M)
+    w, s, b = np_linear(rng, N, K, bits, 64)
+    x = np_x(rng, M, K)
+    xd, wd, sd, bd = to_dev_bf16(x, dev), to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    _lib.call("lisaq_quantized_matmul", torch.cuda.current_stream().cuda_stream, xd.data_ptr(), wd.data_ptr(),
+              sd.data_ptr(), bd.data_ptr(), y.data_ptr(), M, N, K, 1, 64, bits, None, 0)
+    ref = ops.quantized_matmul(xd, wd, sd, bd, True, 64, bits)
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+
+@pytest.mark.parametrize("M,N,K,bits", [(1, 17408, 5120, 4), (1, 3000, 5120, 2), (2, 3001, 5120, 4), (1, 9728, 2560, 4),
+                                        (2, 640, 2048, 2), (1, 100, 1024, 4), (2, 777, 6144, 4)])
+def test_wave_rows_equal_persistent(dev, force_path, M, N, K, bits):
+    """The wave-rows matvec and the persistent matvec share the one-row arithmetic (lane l chains the chunks
+    l, l+64, ... and the same 64-lane sum): every shape both take gives bitwise equal rows, so
+    serial_rows may pair rows in either kernel."""
+    rng = np.random.default_rng(N * 5 + K + M + bits)
+    w, s, b = np_linear(rng, N, K, bits, 64)
+    x = np_x(rng, M, K)
+    force_path("LISAQ_QMV_KERNEL", "s")
+    got_s = _run(ops.qmv, dev, x, w, s, b, 64, bits)
+    force_path("LISAQ_QMV_KERNEL", "p")
+    got_p = _run(ops.qmv, dev, x, w, s, b, 64, bits)
+    assert np.array_equal(got_s, got_p)
+
+
+@pytest.mark.parametrize("N,K", [(264, 5120), (2000, 6144)])
+def test_addnorm_folded_kernels_agree(dev, force_path, N, K):
+    """The add + RMSNorm prologue folded into the wave-rows matvec and into the persistent matvec: the same
+    sum row, normed row and outputs bit for bit (same sum-of-squares order, same matvec arithmetic)."""
+    import torch
+
+    rng = np.random.default_rng(N + 7 * K)
+    w, s, b = np_linear(rng, N, K, 4, 64)
+    from lisa_amd.synth import f32_to_bf16_bits
+    x, r = np_x(rng, 1, K), np_x(rng, 1, K)
+    nw = f32_to_bf16_bits((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    dw = (to_dev_u32(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev))
+    outs = []
+    for k in ("s", "p"):
+        force_path("LISAQ_QMV_KERNEL", k)
+        y, sm, nm = ops.qmv_addnorm(to_dev_bf16(x, dev), to_dev_bf16(r, dev), to_dev_bf16(nw, dev), *dw, 1e-6)
+        torch.cuda.synchronize()
+        outs.append([from_dev_bf16(t) for t in (y, sm, nm)])
+    for a, c in zip(*outs):
+        assert np.array_equal(a, c)
