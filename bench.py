@@ -65,6 +65,9 @@ def main():
                     help="only time the MoE block rows (T=1, 64, 4096) of the configuration table")
     ap.add_argument("--moe-tokens", type=int, nargs="*", default=None,
                     help="with --moe: only these of the MoE rows' token counts (1, 64, 4096)")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only time read-only streams of the configuration rows' byte counts (lisaq_read_stream): "
+                         "the floor a kernel reading those bytes reaches in the same graph replay")
     ap.add_argument("--addnorm", action="store_true",
                     help="only time the residual add + RMSNorm matvec against the plain matvec at the north-star shape")
     args = ap.parse_args()
@@ -95,6 +98,10 @@ def main():
         return
     if args.addnorm:
         addnorm_compare(dev, gen)
+        return
+    if args.read_floor:
+        for r in read_floor(dev):
+            print(json.dumps(r), flush=True)
         return
     if args.moe:
         for r in moe_rows(dev, gen, torch.cuda.Stream(), args.moe_tokens):
@@ -246,6 +253,38 @@ def _time_graph(stream, fn, n_sets, steps, warm_s=CLOCK_WARM_S):
     torch.cuda.synchronize()
     del g
     return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def read_floor(dev):
+    """Read-only streams (lisaq_read_stream: 16-byte nontemporal loads, 1 KB per wave instruction) of the
+    byte counts of the decode rows, over as many rotating buffers as those rows use (> 256 MB, cold), and an
+    empty launch (0 bytes read by one workgroup): per-call time in the same graph replay as the matvec."""
+    import torch
+
+    from lisa_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.Stream()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    rows = []
+    for name, nb, sets in (("configs[1] decode, 4-bit M=1 (9728x2560 / 2560x9728)", qmv_bytes(1, 9728, 2560), 24),
+                           ("2-bit north-star / down shape, M=1", qmv_bytes(1, 17408, 5120, 2), 15),
+                           ("north star 4-bit M=1", qmv_bytes(1, 17408, 5120), 8)):
+        nb16 = nb // 16 * 16
+        bufs = [torch.ones(nb16, dtype=torch.uint8, device=dev) for _ in range(sets)]
+        for L in (1, 2, 4, 8, 16):
+            t = _time_graph(stream, lambda i: _lib.check(lib.lisaq_read_stream(
+                torch.cuda.current_stream().cuda_stream, bufs[i % sets].data_ptr(), nb16, L, sink.data_ptr())),
+                sets, 300)
+            rows.append({"workload": f"read-only stream, {name}", "bytes": nb16, "loads_per_lane": L,
+                         "us": round(t * 1e6, 2), "GB/s": round(nb16 / t / 1e9, 1),
+                         "frac": round(nb16 / t / 1e9 / HBM_PEAK_GBS, 4), "buffers": sets})
+        del bufs
+    one = torch.ones(4096, dtype=torch.uint8, device=dev)
+    t = _time_graph(stream, lambda i: _lib.check(lib.lisaq_read_stream(
+        torch.cuda.current_stream().cuda_stream, one.data_ptr(), 16, 1, sink.data_ptr())), 1, 300)
+    rows.append({"workload": "one-workgroup launch reading 16 bytes (the per-launch floor)", "us": round(t * 1e6, 2)})
+    return rows
 
 
 def addnorm_compare(dev, gen):

@@ -66,6 +66,14 @@ LISAQ_API const char* lisaq_last_error(void);
  * LISAQ_PATH_DEFAULT restores the dispatcher's choice.  Process-wide, read by
  * every later dispatch; never read from the environment.  Unknown name:
  * LISAQ_EINVAL_SHAPE. */
+/* Measurement aid, no counterpart in the reference: a read-only stream of
+ * `bytes` (a multiple of 16 below 2 GiB) of src, 16 bytes per lane,
+ * loads_per_lane (1, 2, 4, 8, 16) consecutive 1 KB pieces per wave,
+ * nontemporal like the matvec's weight loads; nothing is written (sink is
+ * a guard the loads feed, never stored in practice).  The floor a kernel
+ * reading the same bytes can reach, timed by bench.py --read-floor. */
+LISAQ_API int lisaq_read_stream(void* stream, const void* src, size_t bytes, int loads_per_lane, uint32_t* sink);
+
 #define LISAQ_PATH_DEFAULT (-2147483647 - 1)
 LISAQ_API int lisaq_set_path_override(const char* name, int value);
 

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 OUT = os.path.join(HERE, "liblisaq.so")
 OBJ = os.path.join(ROOT, "_build", "lisaq")
-SOURCES = ["qmv.hip", "qmv16.hip", "qmvt.hip", "qmvd.hip", "qmvp.hip", "qmvw.hip", "qmvs.hip", "qmm.hip", "qmm_k4_p.hip", "qmm_k4_s.hip", "qmm_k2_p.hip", "qmm_k2_s.hip", "qmm_gu.hip", "quant.hip", "qtyped.hip", "addnorm.hip", "moe.hip", "moe_decode.hip", "api.cpp"]
+SOURCES = ["qmv.hip", "qmv16.hip", "qmvt.hip", "qmvd.hip", "qmvp.hip", "qmvw.hip", "qmvs.hip", "qmm.hip", "qmm_k4_p.hip", "qmm_k4_s.hip", "qmm_k2_p.hip", "qmm_k2_s.hip", "qmm_gu.hip", "quant.hip", "qtyped.hip", "addnorm.hip", "diag.hip", "moe.hip", "moe_decode.hip", "api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

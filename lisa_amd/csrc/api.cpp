@@ -465,6 +465,13 @@ extern "C" {
 
 int lisaq_version(void) { return 100; }
 
+int lisaq_read_stream(void* stream, const void* src, size_t bytes, int loads_per_lane, uint32_t* sink) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(src && sink, LISAQ_EINVAL_LAYOUT, "read_stream: null pointer");
+  LISAQ_REQUIRE(aligned(src, 16), LISAQ_EINVAL_LAYOUT, "read_stream: src must be 16-byte aligned");
+  return launch_read_stream((hipStream_t)stream, src, bytes, loads_per_lane, sink);
+}
+
 int lisaq_set_path_override(const char* name, int value) {
   const int i = lisaq::path_slot(name);
   LISAQ_REQUIRE(i >= 0, LISAQ_EINVAL_SHAPE, "set_path_override: unknown path %s", name ? name : "(null)");

@@ -59,4 +59,7 @@ int sort_hist_ints(int64_t R, int E);
 int launch_sort_parallel(hipStream_t st, const int32_t* ids, int64_t R, int E, int top_k, int32_t* sorted_idx,
                          int32_t* order, int32_t* token_rows, int32_t* inverse, int32_t* offsets, int32_t* hist);
 
+// measurement aid: read `bytes` of src (16-byte lanes, loads_per_lane 1 KB pieces per wave)
+int launch_read_stream(hipStream_t st, const void* src, size_t bytes, int loads_per_lane, uint32_t* sink);
+
 }  // namespace lisaq

@@ -58,6 +58,20 @@ __device__ __forceinline__ void copy16(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 
 constexpr int kWaves = 4;
 
+// LDS slot of 16-byte x piece P (a 32-code chunk c is pieces 4c .. 4c+3):
+// within each group of 64 pieces (one direct-copy instruction) piece k of
+// chunk c goes to slot 4c + ((k + c + c/4) & 3), so that 16 lanes reading
+// piece k of 16 consecutive chunks hit 16 distinct 4-bank groups (a linear
+// image puts them on 4); the copy reads piece slot^-1 for each slot.
+__device__ __forceinline__ int x_slot(int P) {
+  const int c = (P >> 2) & 15, k = P & 3;
+  return (P & ~63) | (c << 2) | ((k + c + (c >> 2)) & 3);
+}
+__device__ __forceinline__ int x_piece(int slot) {
+  const int c = (slot >> 2) & 15, m = slot & 3;
+  return (slot & ~63) | (c << 2) | ((m - c - (c >> 2)) & 3);
+}
+
 }  // namespace
 
 // Bytes of one wave's staged scales (or biases) region: whole 1 KB copy rounds
@@ -119,7 +133,8 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
     const int xb = (K * 2 * MR) >> 4;
     for (int q0 = 0; q0 < xb; q0 += 256) {  // (uniform)
       const int i = q0 + t;
-      copy16(rx, i < xb ? (uint32_t)i * 16 : kOob, xL + (q0 + wave * 64) * 16);
+      const int pc = x_piece(i);
+      copy16(rx, pc < xb ? (uint32_t)pc * 16 : kOob, xL + (q0 + wave * 64) * 16);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -165,7 +180,7 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
         const uint32_t tt = pack_bf2(bf2f_lo(xv[q][e]) * inv, bf2f_hi(xv[q][e]) * inv);
         gv[q][e] = pack_bf2(bf2f_lo(gv[q][e]) * bf2f_lo(tt), bf2f_hi(gv[q][e]) * bf2f_hi(tt));
       }
-      if (i < KV) *reinterpret_cast<u32x4*>(xL + i * 16) = gv[q];
+      if (i < KV) *reinterpret_cast<u32x4*>(xL + x_slot(i) * 16) = gv[q];
     }
   }
   wait_vm<RW * J>();  // the copies (older than every W load) have landed
@@ -181,7 +196,7 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
       uint32_t raw[16];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const u32x4 v = c < C ? *reinterpret_cast<const u32x4*>(xL + m * K * 2 + c * 64 + 16 * i)
+        const u32x4 v = c < C ? *reinterpret_cast<const u32x4*>(xL + x_slot(m * (K >> 3) + 4 * c + i) * 16)
                               : u32x4{0u, 0u, 0u, 0u};
         raw[4 * i] = v[0];
         raw[4 * i + 1] = v[1];
