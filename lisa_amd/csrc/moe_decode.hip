@@ -172,9 +172,9 @@ __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p)
     }
   }
   uint32_t xp[J][NP];
-  float sx[J], st[J];
+  XSums xs[J];
 #pragma unroll
-  for (int j = 0; j < J; ++j) pair_x<BITS>(raw[j], xp[j], sx[j], st[j]);
+  for (int j = 0; j < J; ++j) pair_x<BITS>(raw[j], xp[j], xs[j]);
   PConst kc;
   kc.init();
 #pragma unroll
@@ -182,10 +182,10 @@ __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p)
     float pg = 0.f, pu = 0.f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const float dg = chunk_dot<BITS>(wg_[rr][j], xp[j], kc);
-      const float du = chunk_dot<BITS>(wu_[rr][j], xp[j], kc);
-      pg = fmaf(bf2f(sg_[rr][j]), dg - 128.0f * st[j], fmaf(bf2f(bg_[rr][j]), sx[j], pg));
-      pu = fmaf(bf2f(su_[rr][j]), du - 128.0f * st[j], fmaf(bf2f(bu_[rr][j]), sx[j], pu));
+      const float dg = chunk_dq<BITS>(wg_[rr][j], xp[j], xs[j], kc);
+      const float du = chunk_dq<BITS>(wu_[rr][j], xp[j], xs[j], kc);
+      pg = fmaf(bf2f(sg_[rr][j]), dg, fmaf(bf2f(bg_[rr][j]), xs[j].sx, pg));
+      pu = fmaf(bf2f(su_[rr][j]), du, fmaf(bf2f(bu_[rr][j]), xs[j].sx, pu));
     }
     const float g = wave_sum(pg), u = wave_sum(pu);
     const int r = r0 + rr;
@@ -252,9 +252,9 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p
     }
   }
   uint32_t xp[P][NP];
-  float sx[P], st[P];
+  XSums xs[P];
 #pragma unroll
-  for (int q = 0; q < P; ++q) pair_x<BITS>(raw[q], xp[q], sx[q], st[q]);
+  for (int q = 0; q < P; ++q) pair_x<BITS>(raw[q], xp[q], xs[q]);
   PConst kc;
   kc.init();
 #pragma unroll
@@ -262,8 +262,8 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p
     float part = 0.f;
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-      const float dq = chunk_dot<BITS>(w_[rr][q], xp[q], kc);
-      part = fmaf(bf2f(s_[rr][q]), dq - 128.0f * st[q], fmaf(bf2f(b_[rr][q]), sx[q], part));
+      const float dq = chunk_dq<BITS>(w_[rr][q], xp[q], xs[q], kc);
+      part = fmaf(bf2f(s_[rr][q]), dq, fmaf(bf2f(b_[rr][q]), xs[q].sx, part));
     }
     const float res = group_sum<LPR>(part);  // every lane of the group holds its expert's dot
     const float prod = valid_e ? __fmul_rn(bf2f(f2bf(res)), wz) : 0.0f;

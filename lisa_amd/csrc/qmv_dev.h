@@ -40,7 +40,8 @@ struct PConst {
 
 // Pairs of one word, each a bf16x2.  4 bits: pair j = (code j, code j+4) as
 // 128+q.  2 bits: pair j = (code j, code j+8) as 128+f*q, f = 1, 4, 16 for
-// j % 3 = 0, 1, 2.
+// j % 3 = 0, 1, 2 (each class summed in its own accumulator and scaled back
+// by 1/f at the chunk's end: dq_finish).
 template <int BITS>
 __device__ __forceinline__ void punpack(uint32_t w, const PConst& k, uint32_t* r) {
   if constexpr (BITS == 4) {
@@ -81,74 +82,88 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 
+// Sums of one chunk's x: sx = sum of x; t[c] = sum of the x paired with the
+// codes of accumulator class c (the 128 offset each class subtracts): 4 bits
+// one class (t[0] = sx); 2 bits three classes, pairs q % 3 == 0, 1, 2, whose
+// codes sit at mantissa bits 0-1, 2-3 and 4-5 (values 128 + q, 128 + 4 q,
+// 128 + 16 q).
+struct XSums {
+  float sx;
+  float t[3];
+};
+
+// accumulator class of pair q of a word (and the number of classes)
+template <int BITS>
+__device__ __forceinline__ constexpr int acc_class(int q) { return BITS == 4 ? (q & 1) : q % 3; }
+template <int BITS>
+constexpr int kAccClasses = BITS == 4 ? 2 : 3;
+
 // x of one 32-code chunk (16 bf16 pairs in raw[16], element 2i in the low
 // half of raw[i]) paired in unpack order: xp[wd * PPW + q] holds the x of the
-// two codes that punpack<BITS> puts in pair q of word wd (2 bits: scaled by
-// 1, 1/4, 1/16 as the pair's code shift).  sx = sum of x, st = sum of the
-// scaled x (st = sx at 4 bits); both are bf16 dot products with (1, 1), one
-// instruction per pair (the scaled values are exact in bf16: powers of two).
+// two codes that punpack<BITS> puts in pair q of word wd (one byte permute
+// each: both values are the same halves of two raw words); sums as XSums
+// (bf16 dot products with (1, 1)).
 template <int BITS>
-__device__ __forceinline__ void pair_x(const uint32_t* raw, uint32_t* xp, float& sx, float& st) {
+__device__ __forceinline__ void pair_x(const uint32_t* raw, uint32_t* xp, XSums& xs) {
   constexpr int WPC = BITS == 4 ? 4 : 2;  // words per chunk
   constexpr int PPW = 16 / BITS;          // pairs per word
+  constexpr int HALF = PPW / 2;           // raw words between a pair's two x
   constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
-  auto xval = [&](int k) -> uint32_t { return (k & 1) ? (raw[k >> 1] >> 16) : (raw[k >> 1] & 0xffffu); };
 #pragma unroll
   for (int wd = 0; wd < WPC; ++wd)
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
-      uint32_t lo, hi;
-      if constexpr (BITS == 4) {
-        // x[8wd+q] and x[8wd+q+4] are the same halves of raw[4wd+q/2] and
-        // raw[4wd+q/2+2]: one byte permute
-        const uint32_t a = raw[4 * wd + q / 2], b = raw[4 * wd + q / 2 + 2];
-        xp[wd * PPW + q] = __builtin_amdgcn_perm(b, a, (q & 1) ? 0x07060302u : 0x05040100u);
-        continue;
-      } else {
-        const int fq = q % 3;
-        const float f = fq == 0 ? 1.0f : (fq == 1 ? 0.25f : 0.0625f);
-        lo = __float_as_uint(__uint_as_float(xval(16 * wd + q) << 16) * f) >> 16;  // power of two: exact
-        hi = __float_as_uint(__uint_as_float(xval(16 * wd + q + 8) << 16) * f) >> 16;
-      }
-      xp[wd * PPW + q] = lo | (hi << 16);
+      // pair q of word wd: x[PPW*2*wd + q] and x[PPW*2*wd + q + PPW], the same
+      // halves of raw[PPW*wd + q/2] and raw[PPW*wd + q/2 + HALF]
+      const uint32_t a = raw[PPW * wd + q / 2], b = raw[PPW * wd + q / 2 + HALF];
+      xp[wd * PPW + q] = __builtin_amdgcn_perm(b, a, (q & 1) ? 0x07060302u : 0x05040100u);
     }
-  float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; i += 2) {
-    a0 = pdot2(raw[i], kOnes, a0);
-    a1 = pdot2(raw[i + 1], kOnes, a1);
-  }
-  sx = a0 + a1;
   if constexpr (BITS == 4) {
-    st = sx;
-  } else {
-    float t0 = 0.f, t1 = 0.f;
+    float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < WPC * PPW; i += 2) {
-      t0 = pdot2(xp[i], kOnes, t0);
-      t1 = pdot2(xp[i + 1], kOnes, t1);
+    for (int i = 0; i < 16; i += 2) {
+      a0 = pdot2(raw[i], kOnes, a0);
+      a1 = pdot2(raw[i + 1], kOnes, a1);
     }
-    st = t0 + t1;
+    xs.sx = a0 + a1;
+    xs.t[0] = xs.t[1] = xs.t[2] = xs.sx;
+  } else {
+    float t[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < WPC * PPW; ++i) t[(i % PPW) % 3] = pdot2(xp[i], kOnes, t[(i % PPW) % 3]);
+    xs.t[0] = t[0];
+    xs.t[1] = t[1];
+    xs.t[2] = t[2];
+    xs.sx = (t[0] + t[1]) + t[2];  // every x of the chunk is in exactly one class
   }
 }
 
-// sum(x * (128 + q)) of one chunk: the chunk's words w[WPC] against xp
+// sum(x * q) of one chunk from its class accumulators acc[c] = sum of
+// x * (128 + f_c q) over the class's pairs (f_c = 1, 4, 16 at 2 bits; one
+// class 1 at 4 bits, accumulated in two halves)
 template <int BITS>
-__device__ __forceinline__ float chunk_dot(const uint32_t* w, const uint32_t* xp, const PConst& k) {
+__device__ __forceinline__ float dq_finish(const float* acc, const XSums& xs) {
+  if constexpr (BITS == 4) {
+    return (acc[0] + acc[1]) - 128.0f * xs.t[0];
+  } else {
+    return ((acc[0] - 128.0f * xs.t[0]) + (acc[1] - 128.0f * xs.t[1]) * 0.25f) + (acc[2] - 128.0f * xs.t[2]) * 0.0625f;
+  }
+}
+
+// sum(x * q) of one chunk: the chunk's words w[WPC] against xp
+template <int BITS>
+__device__ __forceinline__ float chunk_dq(const uint32_t* w, const uint32_t* xp, const XSums& xs, const PConst& k) {
   constexpr int WPC = BITS == 4 ? 4 : 2;
   constexpr int PPW = 16 / BITS;
-  float d0 = 0.f, d1 = 0.f;
+  float acc[3] = {0.f, 0.f, 0.f};
 #pragma unroll
   for (int wd = 0; wd < WPC; ++wd) {
     uint32_t r[PPW];
     punpack<BITS>(w[wd], k, r);
 #pragma unroll
-    for (int q = 0; q < PPW; ++q) {
-      if (q & 1) d1 = pdot2(r[q], xp[wd * PPW + q], d1);
-      else d0 = pdot2(r[q], xp[wd * PPW + q], d0);
-    }
+    for (int q = 0; q < PPW; ++q) acc[acc_class<BITS>(q)] = pdot2(r[q], xp[wd * PPW + q], acc[acc_class<BITS>(q)]);
   }
-  return d0 + d1;
+  return dq_finish<BITS>(acc, xs);
 }
 
 }  // namespace qmvdev

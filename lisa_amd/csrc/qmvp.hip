@@ -229,11 +229,11 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
 
   // --- x paired in unpack order, with sums (per row of x)
   uint32_t xp[MR][J][NP];
-  float sx[MR][J], st[MR][J];
+  XSums xs[MR][J];
 #pragma unroll
   for (int r = 0; r < MR; ++r)
 #pragma unroll
-    for (int j = 0; j < J; ++j) pair_x<BITS>(raw[r][j], xp[r][j], sx[r][j], st[r][j]);
+    for (int j = 0; j < J; ++j) pair_x<BITS>(raw[r][j], xp[r][j], xs[r][j]);
 
   PConst kc;
   kc.init();
@@ -250,9 +250,9 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
     for (int r = 0; r < MR; ++r) part[r] = 0.f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      float d0[MR], d1[MR];
+      float acc[MR][3];
 #pragma unroll
-      for (int r = 0; r < MR; ++r) d0[r] = d1[r] = 0.f;
+      for (int r = 0; r < MR; ++r) acc[r][0] = acc[r][1] = acc[r][2] = 0.f;
 #pragma unroll
       for (int wd = 0; wd < WPC; ++wd) {
         uint32_t rq[PPW];
@@ -260,15 +260,14 @@ __global__ __launch_bounds__(256) void qmvp_kernel(QmvParams p) {
 #pragma unroll
         for (int r = 0; r < MR; ++r)
 #pragma unroll
-          for (int q = 0; q < PPW; ++q) {
-            if (q & 1) d1[r] = pdot2(rq[q], xp[r][j][wd * PPW + q], d1[r]);
-            else d0[r] = pdot2(rq[q], xp[r][j][wd * PPW + q], d0[r]);
-          }
+          for (int q = 0; q < PPW; ++q)
+            acc[r][acc_class<BITS>(q)] = pdot2(rq[q], xp[r][j][wd * PPW + q], acc[r][acc_class<BITS>(q)]);
       }
       const float s = bf2f(*reinterpret_cast<const uint16_t*>(sbl + gofs[j]));
       const float b = bf2f(*reinterpret_cast<const uint16_t*>(sbl + G2 + gofs[j]));
 #pragma unroll
-      for (int r = 0; r < MR; ++r) part[r] = fmaf(s, (d0[r] + d1[r]) - 128.0f * st[r][j], fmaf(b, sx[r][j], part[r]));
+      for (int r = 0; r < MR; ++r)
+        part[r] = fmaf(s, dq_finish<BITS>(acc[r], xs[r][j]), fmaf(b, xs[r][j].sx, part[r]));
     }
 #pragma unroll
     for (int r = 0; r < MR; ++r) {

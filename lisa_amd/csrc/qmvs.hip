@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
   lds_sync();
 
   uint32_t xp[MR][J][NP];
-  float sx[MR][J], st[MR][J];
+  XSums xs[MR][J];
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
         raw[4 * i + 2] = v[2];
         raw[4 * i + 3] = v[3];
       }
-      pair_x<BITS>(raw, xp[m][j], sx[m][j], st[m][j]);
+      pair_x<BITS>(raw, xp[m][j], xs[m][j]);
     }
 
   // --- 3. rows in issue order: the one-row kernel's chain and row sum
@@ -228,9 +228,9 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
       const float s = bf2f(*reinterpret_cast<const uint16_t*>(sL + i * G * 2 + gofs[j]));
       const float b = bf2f(*reinterpret_cast<const uint16_t*>(bL + i * G * 2 + gofs[j]));
       const uint32_t* wp = reinterpret_cast<const uint32_t*>(&wv[i][j]);
-      float d0[MR], d1[MR];
+      float acc[MR][3];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) d0[m] = d1[m] = 0.f;
+      for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = acc[m][2] = 0.f;
 #pragma unroll
       for (int wd = 0; wd < WPC; ++wd) {
         uint32_t rq[PPW];
@@ -238,14 +238,12 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
-          for (int q = 0; q < PPW; ++q) {
-            if (q & 1) d1[m] = pdot2(rq[q], xp[m][j][wd * PPW + q], d1[m]);
-            else d0[m] = pdot2(rq[q], xp[m][j][wd * PPW + q], d0[m]);
-          }
+          for (int q = 0; q < PPW; ++q)
+            acc[m][acc_class<BITS>(q)] = pdot2(rq[q], xp[m][j][wd * PPW + q], acc[m][acc_class<BITS>(q)]);
       }
 #pragma unroll
       for (int m = 0; m < MR; ++m)
-        part[m] = fmaf(s, (d0[m] + d1[m]) - 128.0f * st[m][j], fmaf(b, sx[m][j], part[m]));
+        part[m] = fmaf(s, dq_finish<BITS>(acc[m], xs[m][j]), fmaf(b, xs[m][j].sx, part[m]));
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
