@@ -54,6 +54,9 @@ struct MoeDecodeParams {
 // gate|up 2 / down 2 rows per wave 15.2 us, down 1: 14.1, gate|up 4: 16.8, gate|up 1: 16.9, down 4: 18.7
 constexpr int kRpwGu = 2, kRpwDc = 1;
 
+// bytes of the gate|up kernel's LDS copy of x (whole 4 KB copy rounds)
+__host__ __device__ inline int xl_bytes(int H) { return (H * 2 + 4095) / 4096 * 4096; }
+
 __device__ __forceinline__ void copy16_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, void* lds) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 }
@@ -112,25 +115,38 @@ __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p)
         for (int i = 0; i < 16; ++i) raw[j][i] = 0;
     }
   }
-  // the token's routing (every wave routes its token: no separate router
-  // launch); slot jz's expert.  One wave per token writes the ids and weights
-  // for the down kernel and the caller.
-  int e;
-  {
+  // the token's routing (no separate router launch); slot jz's expert.  One
+  // wave per token writes the ids and weights for the down kernel and the
+  // caller.  XS: wave 0 of the workgroup routes (the workgroup's waves share
+  // the slot), and only as far as the slot's rank; the other waves take the
+  // expert from LDS after the barrier (the routing's VALU work, done by every
+  // wave of every workgroup, took ~3.7 us of a 13.9 us block at T = 1)
+  int e = 0;
+  const bool writer = blockIdx.x == 0 && jz == 0;
+  if (!XS || wave == 0) {
     int sid;
-    float w;
-    route_wave<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, lane, sid, w);
+    if (writer) {
+      float w;
+      route_wave<PER>(p.logits + (int64_t)t * p.E, p.E, p.k, lane, sid, w);
+      if (wave == 0 && lane < p.k) {
+        p.idx[(int64_t)t * p.k + lane] = sid;
+        p.wts[(int64_t)t * p.k + lane] = w;
+      }
+    } else {
+      float sel;
+      route_select<PER>(p.logits + (int64_t)t * p.E, p.E, jz + 1, lane, sid, sel);
+    }
     e = __builtin_amdgcn_readlane(sid, jz);
-    if (blockIdx.x == 0 && wave == 0 && jz == 0 && lane < p.k) {
-      p.idx[(int64_t)t * p.k + lane] = sid;
-      p.wts[(int64_t)t * p.k + lane] = w;
+    if constexpr (XS) {
+      if (lane == 0) *reinterpret_cast<int*>(xl + xl_bytes(p.H)) = e;
     }
   }
-  const bool valid_e = e >= 0 && e < p.E;
   if constexpr (XS) {
-    // the routing waited for its logits, issued after the copies: they have landed
+    // wave 0's routing waited for its logits, issued after the copies: they
+    // have landed there; the other waves wait for their own copies here
     __builtin_amdgcn_s_waitcnt(0);  // (the copies are not tracked by the compiler's waits)
     __syncthreads();
+    e = *reinterpret_cast<const int*>(xl + xl_bytes(p.H));
     if (r0 >= p.I) return;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -148,6 +164,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p)
     }
   }
   // every row's W words, scales and biases
+  const bool valid_e = e >= 0 && e < p.E;
   uint32_t wg_[RPW][J][WPC], wu_[RPW][J][WPC];
   uint16_t sg_[RPW][J], bg_[RPW][J], su_[RPW][J], bu_[RPW][J];
   const int64_t ebase = valid_e ? (int64_t)e * p.I : 0;
@@ -358,7 +375,7 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, in
   moe_fn gu = by_format(bits, gs, [&](auto B, auto S) { return pick_gu<decltype(B)::value, decltype(S)::value>(J, E); });
   moe_fn dc = by_format(bits, gs, [&](auto B, auto S) { return pick_dc<decltype(B)::value, decltype(S)::value>(k, P); });
   if (!gu || !dc) return set_error(LISAQ_EUNSUPPORTED, "moe decode: no kernel for J=%d P=%d k=%d", J, P, k);
-  const int xlds = kGuXs ? (int)((H * 2 + 4095) / 4096 * 4096) : 0;
+  const int xlds = kGuXs ? xl_bytes((int)H) + 16 : 0;
   hipLaunchKernelGGL(gu, dim3((unsigned)((I + 4 * kRpwGu - 1) / (4 * kRpwGu)), (unsigned)(T * k)), dim3(256), xlds, st, p);
   int rc = check_launch("moe_gate_up_act");
   if (rc) return rc;

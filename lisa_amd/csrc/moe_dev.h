@@ -62,6 +62,68 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 
+// wave maximum of an int32, broadcast (the ladder of wave_max)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int route_dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp((int)0x80000000, x, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ int wave_max_i32(int v) {
+  v = max(v, route_dpp_i<0xB1, 0xF>(v));
+  v = max(v, route_dpp_i<0x4E, 0xF>(v));
+  v = max(v, route_dpp_i<0x141, 0xF>(v));
+  v = max(v, route_dpp_i<0x140, 0xF>(v));
+  v = max(v, route_dpp_i<0x142, 0xA>(v));
+  v = max(v, route_dpp_i<0x143, 0xC>(v));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// The first `rounds` rounds of the top-k selection (rounds <= 64): lane r <
+// rounds gets the expert of rank r in sid_out and its logit in sel_out.  The
+// logits are compared as order-preserving int32 keys (a float's bits, the
+// magnitude bits flipped for negative values; NaN taken as -inf and -0 as
+// +0 first), so each round is integer maxima and ballots: no NaN-quieting
+// around every comparison.  A taken or absent expert has the key INT_MIN,
+// below every logit's (-inf's is 0x807FFFFF).
+template <int PER>
+__device__ __forceinline__ void route_select(const float* __restrict__ l, int E, int rounds, int lane, int& sid_out,
+                                             float& sel_out) {
+  constexpr int kNone = (int)0x80000000;
+  int key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    const float x = e < E ? l[e] : -INFINITY;
+    const float v = x != x ? -INFINITY : x + 0.0f;  // NaN -> -inf; -0 -> +0
+    const int b = __float_as_int(v);
+    key[i] = e < E ? (b >= 0 ? b : b ^ 0x7FFFFFFF) : kNone;
+  }
+  // lane r keeps round r's winner
+  int mykey = kNone, mysid = 0;
+  for (int r = 0; r < rounds; ++r) {
+    int best = key[0];
+#pragma unroll
+    for (int i = 1; i < PER; ++i) best = max(best, key[i]);
+    const int m = wave_max_i32(best);
+    // the lowest expert id with key m: lowest slot, then lowest lane
+    int win = -1;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint64_t bal = __ballot(key[i] == m);
+      if (win < 0 && bal != 0) win = i * 64 + (int)__builtin_ctzll(bal);
+    }
+    if (win < 0) win = 0;  // (only when fewer than k experts remain; k <= E is checked on the host)
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (win == i * 64 + lane) key[i] = kNone;
+    if (lane == r) {
+      mykey = m;
+      mysid = win;
+    }
+  }
+  sid_out = mysid;
+  sel_out = __int_as_float(mykey >= 0 ? mykey : mykey ^ 0x7FFFFFFF);
+}
+
 // Top-k routing of one token by one wave (the router's arithmetic): lane r < k
 // gets the expert of rank r (largest logit first, ties to the lower id; a NaN
 // logit counts as -inf) and its weight of the softmax over the k selected
@@ -70,43 +132,8 @@ __device__ __forceinline__ float wave_max(float v) {
 template <int PER>
 __device__ __forceinline__ void route_wave(const float* __restrict__ l, int E, int k, int lane, int& sid_out,
                                            float& w_out) {
-  float v[PER];
-  uint32_t taken = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e = lane + 64 * i;
-    const float x = e < E ? l[e] : -INFINITY;
-    v[i] = x != x ? -INFINITY : x + 0.0f;  // NaN -> -inf; -0 -> +0
-    if (e >= E) taken |= 1u << i;
-  }
-  // lane r keeps round r's winner (k <= 64)
-  float mysel = -INFINITY;
-  int mysid = 0;
-  for (int r = 0; r < k; ++r) {
-    // lane-local best not yet taken (scanning upward keeps the lowest slot on ties)
-    float best = -INFINITY;
-    int bslot = -1;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const bool ok = !(taken & (1u << i)) && (bslot < 0 || v[i] > best);
-      best = ok ? v[i] : best;
-      bslot = ok ? i : bslot;
-    }
-    const float m = wave_max(bslot >= 0 ? best : -INFINITY);
-    // the lowest expert id with value m: lowest slot, then lowest lane
-    int win = -1;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const uint64_t bal = __ballot(bslot == i && best == m);
-      if (win < 0 && bal != 0) win = i * 64 + (int)__builtin_ctzll(bal);
-    }
-    if (win < 0) win = 0;  // (only when fewer than k experts remain; k <= E is checked on the host)
-    if ((win & 63) == lane) taken |= 1u << (win >> 6);
-    if (lane == r) {
-      mysel = m;
-      mysid = win;
-    }
-  }
+  float mysel;
+  route_select<PER>(l, E, k, lane, sid_out, mysel);
   // softmax over the k selected logits: max, then exp and the sum in round
   // order, w = e * (1/sum)
   const float mx = wave_max(lane < k ? mysel : -INFINITY);
@@ -114,7 +141,6 @@ __device__ __forceinline__ void route_wave(const float* __restrict__ l, int E, i
   float sum = 0.f;
   for (int r = 0; r < k; ++r) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
   const float inv = 1.0f / sum;
-  sid_out = mysid;
   w_out = ex * inv;
 }
 
