@@ -228,25 +228,30 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = blockIdx.y;
   const int d0 = (blockIdx.x * 4 + wave) * RPW;
-  if (d0 >= p.H) return;
   const int jx = lane / LPR, sub = lane % LPR;  // expert slot and lane within its row
   const int z = t * KE + jx;
   const int C = p.I / 32, G = p.I / GS;
   const int64_t wrow = p.I / PACK;
-  // the activations of the lane's chunks first (paired after every load is
-  // in flight), then the expert id and weight
-  uint32_t raw[P][16];
-#pragma unroll
-  for (int q = 0; q < P; ++q) {
-    const int c = sub + LPR * q;
-    if (c < C) load_x_chunk(p.act + (int64_t)z * p.I + c * 32, raw[q]);
-    else
-#pragma unroll
-      for (int i = 0; i < 16; ++i) raw[q][i] = 0;
+  // the token's k activation rows (contiguous) copied once per workgroup into
+  // LDS (every wave read all of them from L2 before: 4x the bytes); they are
+  // read back after the barrier
+  extern __shared__ __attribute__((aligned(16))) unsigned char al[];
+  {
+    const int ab = KE * p.I * 2 / 16;  // 16-byte pieces (I % 32 == 0)
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.act + (int64_t)t * KE * p.I, (uint32_t)ab * 16);
+    for (int q0 = 0; q0 < ab; q0 += 256) {
+      const int i = q0 + (int)threadIdx.x;
+      copy16_lds(ra, i < ab ? (uint32_t)i * 16 : kOob, al + (q0 + wave * 64) * 16);
+    }
   }
+  asm volatile("" ::: "memory");  // the id load below stays behind the copies
+  __builtin_amdgcn_sched_barrier(0);
+  // the expert id and weight (their wait also covers the wave's copies,
+  // issued before them), then every load of the rows; the barrier publishes
+  // the other waves' copies
   const int e = p.idx[z];
-  const bool valid_e = e >= 0 && e < p.E;
   const float wz = p.wts[z];
+  const bool valid_e = e >= 0 && e < p.E;
   uint32_t w_[RPW][P][WPC];
   uint16_t s_[RPW][P], b_[RPW][P];
   const int64_t ebase = valid_e ? (int64_t)e * p.H : 0;
@@ -266,6 +271,23 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p
         for (int i = 0; i < WPC; ++i) w_[rr][q][i] = 0;
         s_[rr][q] = b_[rr][q] = 0;
       }
+    }
+  }
+  asm volatile("s_barrier" ::: "memory");
+  if (d0 >= p.H) return;
+  uint32_t raw[P][16];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    const int c = sub + LPR * q;
+    if (c < C) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(al + (jx * p.I + c * 32) * 2 + 16 * i);
+        raw[q][4 * i] = v[0]; raw[q][4 * i + 1] = v[1]; raw[q][4 * i + 2] = v[2]; raw[q][4 * i + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) raw[q][i] = 0;
     }
   }
   uint32_t xp[P][NP];
@@ -357,6 +379,7 @@ bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int E, int k, int gs,
   if (!(k == 1 || k == 2 || k == 4 || k == 8 || k == 16)) return false;
   if (!(bits == 2 || bits == 4) || !(gs == 32 || gs == 64 || gs == 128)) return false;
   if (H % gs || I % gs) return false;
+  if ((int64_t)k * I * 2 > 160 * 1024) return false;  // the down kernel's activations in LDS
   const int P = down_passes(I, k);
   return P == 1 || P == 2 || P == 3 || P == 4 || P == 6 || P == 8;
 }
@@ -379,7 +402,9 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, in
   hipLaunchKernelGGL(gu, dim3((unsigned)((I + 4 * kRpwGu - 1) / (4 * kRpwGu)), (unsigned)(T * k)), dim3(256), xlds, st, p);
   int rc = check_launch("moe_gate_up_act");
   if (rc) return rc;
-  hipLaunchKernelGGL(dc, dim3((unsigned)((H + 4 * kRpwDc - 1) / (4 * kRpwDc)), (unsigned)T), dim3(256), 0, st, p);
+  const int alds = (int)((k * I * 2 + 4095) / 4096 * 4096);
+  if (int rc2 = allow_dyn_lds((const void*)dc, alds, "moe_down_combine")) return rc2;
+  hipLaunchKernelGGL(dc, dim3((unsigned)((H + 4 * kRpwDc - 1) / (4 * kRpwDc)), (unsigned)T), dim3(256), alds, st, p);
   return check_launch("moe_down_combine");
 }
 
