@@ -62,7 +62,8 @@ LISAQ_API const char* lisaq_last_error(void);
  * for the shapes it accepts).  Names: LISAQ_QMV_KERNEL (value = the kernel's
  * letter 'w','p','d','t','1' (16-row),'3' (32-row); a shape the kernel does
  * not take falls through to the next), LISAQ_QMM_SPLIT (matmul parts over K),
- * LISAQ_GATHER_SHORT, LISAQ_MOE_GU, LISAQ_MOE_FUSED, LISAQ_MOE_GU_MV (0 = off).
+ * LISAQ_GATHER_SHORT, LISAQ_MOE_GU, LISAQ_MOE_FUSED (2 one launch, 1 two
+ * launches), LISAQ_MOE_GU_MV (0 = off).
  * LISAQ_PATH_DEFAULT restores the dispatcher's choice.  Process-wide, read by
  * every later dispatch; never read from the environment.  Unknown name:
  * LISAQ_EINVAL_SHAPE. */
@@ -242,17 +243,22 @@ LISAQ_API int lisaq_moe_combine(void* stream, const void* down_sorted, const flo
  * topk_idx/topk_weights [T,k] may be NULL.
  * Few tokens (lisaq_moe_decode_supported: T <= 8, the engine's decode window,
  * moe.rs:263-332, 415-420) take the fused decode path of moe_decode.rs
- * (routing + gate|up + SwiGLU, then down + combine: two launches),
- * with the same rounding points; the environment variable LISAQ_MOE_FUSED=0
- * selects the generic path instead.  Many tokens (T*k >= 20*E, H % 64 == 0,
- * I % 64 == 0) take lisaq_gather_qmm_swiglu for gate|up + SwiGLU (one launch,
- * x read through the sort's row map); LISAQ_MOE_GU=0 selects the path below.
+ * (routing + gate|up + SwiGLU, then down + combine, in one launch whose
+ * down workgroups wait for their token's gate|up workgroups' flags), with the same
+ * rounding points; the path override LISAQ_MOE_FUSED (lisaq_set_path_override)
+ * 1 selects two launches (the same arithmetic), 0 the generic path.  Many
+ * tokens (T*k >= 20*E, H % 64 == 0, I % 64 == 0) take
+ * lisaq_gather_qmm_swiglu for gate|up + SwiGLU (one launch, x read through
+ * the sort's row map); LISAQ_MOE_GU=0 selects the path below.
  * Between the two: gate|up + SwiGLU of the runs shorter than
  * qmv_batch_limit(H, I) in one matvec launch per run-length class (matvec
  * arithmetic), of the longer runs in the gate|up matmul, x read through the
  * row map -- bitwise equal to the three-step gather, gate, up, SwiGLU
  * sequence, which LISAQ_MOE_GU_MV=0 selects.
- * workspace: lisaq_moe_workspace() bytes, zero-filled before first use. */
+ * workspace: lisaq_moe_workspace() bytes, zero-filled before first use.  Its
+ * first 4 bytes are set to 1 if a one-launch wait ever gave up (not expected:
+ * workgroups are dispatched in block order); that call's output is then not
+ * valid.  Calls that share a workspace are ordered on one stream. */
 LISAQ_API int lisaq_moe_forward(void* stream, const void* x, const float* logits, const uint32_t* gate_w,
                       const void* gate_s, const void* gate_b, const uint32_t* up_w,
                       const void* up_s, const void* up_b, const uint32_t* down_w,

@@ -997,7 +997,7 @@ int lisaq_moe_combine(void* stream, const void* down, const float* wts, const in
 
 // MoE forward workspace: [routing ints][x_sorted][gate_out][up_out][down_sorted][gather ws]
 struct MoeLayout {
-  size_t idx, wts, sorted, order, rows, inv, offs, hist, xs, g, u, d, gws, total;
+  size_t err, flags, idx, wts, sorted, order, rows, inv, offs, hist, xs, g, u, d, gws, total;
 };
 
 // The down projection of the fused-gate|up prefill takes kTallBM-row matmul
@@ -1016,6 +1016,8 @@ static MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int E, int k, int g
     o += up256(bytes);
     return at;
   };
+  L.err = take(256);  // first, at the same place for every T: the one-launch decode's give-up word
+  L.flags = take((size_t)moe_decode_flags(T, I, k) * 8);
   L.idx = take((size_t)R * 4);
   L.wts = take((size_t)R * 4);
   L.sorted = take((size_t)R * 4);
@@ -1076,15 +1078,18 @@ int lisaq_moe_forward(void* stream, const void* x, const float* logits, const ui
   void* gws = B + L.gws;
   const size_t gws_bytes = L.total - L.gws;
   int rc;
-  // Few tokens (T <= 8, the reference's decode window): fused path, two
-  // launches, the first one routing (LISAQ_MOE_FUSED=0 selects the generic path)
-  if (path_int("LISAQ_MOE_FUSED", 1) != 0 && moe_decode_supported(T, H, I, E, k, gs, bits)) {
+  // Few tokens (T <= 8, the reference's decode window): fused path, routing
+  // inside; LISAQ_MOE_FUSED 2 (default) one launch, 1 two launches, 0 the
+  // generic path
+  const int fused = path_int("LISAQ_MOE_FUSED", 2);
+  if (fused != 0 && moe_decode_supported(T, H, I, E, k, gs, bits)) {
     if ((rc = validate_mm("moe_forward gate", x, gw, gsc, gbi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward up", x, uw, usc, ubi, g, R, I, H, 1, gs, bits))) return rc;
     if ((rc = validate_mm("moe_forward down", g, dw, dsc, dbi, out, R, H, I, 1, gs, bits))) return rc;
     return launch_moe_decode(st, (const uint16_t*)x, logits, idx, wts, gw, (const uint16_t*)gsc, (const uint16_t*)gbi, uw,
                              (const uint16_t*)usc, (const uint16_t*)ubi, dw, (const uint16_t*)dsc,
-                             (const uint16_t*)dbi, g, (uint16_t*)out, T, H, I, E, k, gs, bits);
+                             (const uint16_t*)dbi, g, (uint16_t*)out, T, H, I, E, k, gs, bits,
+                             fused == 2 ? (uint64_t*)(B + L.flags) : nullptr, (uint32_t*)(B + L.err));
   }
   if ((rc = lisaq_moe_route(st, logits, T, E, k, idx, wts))) return rc;
   LISAQ_REQUIRE(E <= 1024, LISAQ_EINVAL_SHAPE, "moe_forward: need E <= 1024 (E=%d)", E);

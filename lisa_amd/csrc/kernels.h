@@ -20,13 +20,16 @@ int launch_add_rms(hipStream_t st, const uint16_t* x, const uint16_t* r, const u
 int launch_swiglu(hipStream_t st, const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n);
 int launch_combine(hipStream_t st, const uint16_t* down, const float* w, const int32_t* inv,
                    uint16_t* out, int64_t T, int k, int64_t H);
-// fused decode MoE (moe_decode.hip): routing + gate|up + SwiGLU, then down + combine
+// fused decode MoE (moe_decode.hip): routing + gate|up + SwiGLU, then down +
+// combine; flags null: two launches, else one launch with
+// moe_decode_flags(T, I, k) flags (any contents) and a give-up word err
 bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits);
 int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, int32_t* idx, float* wts,
                       const uint32_t* gw, const uint16_t* gsc, const uint16_t* gbi, const uint32_t* uw,
                       const uint16_t* usc, const uint16_t* ubi, const uint32_t* dw, const uint16_t* dsc,
                       const uint16_t* dbi, uint16_t* act, uint16_t* out, int64_t T, int64_t H, int64_t I, int E,
-                      int k, int gs, int bits);
+                      int k, int gs, int bits, uint64_t* flags, uint32_t* err);
+int64_t moe_decode_flags(int64_t T, int64_t I, int k);
 // quantized matmul for f16/f32/bf16 and 2/4/8-bit codes (qtyped.hip): the
 // matvec arithmetic when matvec, else the matmul arithmetic
 int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* w, const void* s, const void* b,

@@ -1,5 +1,5 @@
-// Fused decode MoE (few tokens): gate|up matvec + SwiGLU in one launch, down
-// matvec + weighted combine in another, after the router.
+// Fused decode MoE (few tokens): gate|up matvec + SwiGLU and down matvec +
+// weighted combine, routing inside, in one launch (k = 2, 4, 8) or two.
 //
 // Reference: the engine's one-token decode MoE, track_moe_route_1 ->
 // track_moe_gate_up_reuse_2row -> track_moe_down_combine_1
@@ -22,6 +22,11 @@
 // The routing sits between the launch and the first weight load (the experts
 // are not known before it): with a fixed expert set instead (experiment build)
 // the block took 10.0 us instead of 13.9 at T = 1, E = 128, k = 8.
+// One launch: gate|up workgroups first in block order, then down workgroups
+// that route for themselves, issue their weight loads, and wait on per-
+// workgroup flags (tagged with the dispatch id) for their token's rows; the
+// rows travel write-through (sc1 stores and loads) so no cache write-back or
+// invalidation is needed (11.1 vs 11.5 us for two launches at T = 1).
 // down_combine: each wave RPW output rows of H; the k experts of the token are
 // side by side in the wave (64/k lanes per expert row), the partial dot
 // products are summed within each lane group, and the k results are folded
@@ -47,6 +52,11 @@ struct MoeDecodeParams {
   uint16_t* act;        // [T*k, I] bf16
   uint16_t* out;        // [T, H] bf16
   int T, H, I, E, k;
+  // one launch: a flag per gate|up workgroup, the give-up word, gate|up
+  // blocks (gu_x per slot, n_gu in all), down blocks (dc_x per token, n_dc)
+  uint64_t* flags;
+  uint32_t* err;
+  int gu_x, n_gu, dc_x, n_dc, gu_per_token;
 };
 
 // rows per wave: gate|up (each row both a gate and an up row) and down
@@ -57,8 +67,10 @@ constexpr int kRpwGu = 2, kRpwDc = 1;
 // bytes of the gate|up kernel's LDS copy of x (whole 4 KB copy rounds)
 __host__ __device__ inline int xl_bytes(int H) { return (H * 2 + 4095) / 4096 * 4096; }
 
+// AUX: the load's cache policy bits (16: sc1, read at the device's coherence point)
+template <int AUX = 0>
 __device__ __forceinline__ void copy16_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, void* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, AUX);
 }
 
 // one chunk (32 codes) of a W row: 16 bytes at 4 bits, 8 at 2
@@ -82,21 +94,66 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* p, uint32_t* raw) {
   }
 }
 
-template <int BITS, int GS, int J, int PER, int RPW, bool XS>
-__global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p) {
+// the token's k activation rows [k, I] (contiguous) into LDS, 16 bytes per
+// lane; lanes past the end write zeros into the padding of the last round
+template <int KE, int AUX>
+__device__ __forceinline__ void copy_act(const MoeDecodeParams& p, int t, unsigned char* al, int wave) {
+  const int ab = KE * p.I * 2 / 16;  // 16-byte pieces (I % 32 == 0)
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.act + (int64_t)t * KE * p.I, (uint32_t)ab * 16);
+  for (int q0 = 0; q0 < ab; q0 += 256) {
+    const int i = q0 + (int)threadIdx.x;
+    copy16_lds<AUX>(ra, i < ab ? (uint32_t)i * 16 : kOob, al + (q0 + wave * 64) * 16);
+  }
+}
+
+// One launch: gate|up workgroup b stores this launch's tag in flags[b] once
+// its rows are stored; a down workgroup waits until every flag of its token
+// holds the tag.  The tag is unique per dispatch (the packet's dispatch id
+// on its queue, mixed with the queue's address), so flags left by earlier
+// launches never match and nothing is ever reset.
+extern "C" __device__ uint64_t lisaq_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
+__device__ __forceinline__ uint64_t launch_tag() {
+  return lisaq_dispatch_id() * 0x9E3779B97F4A7C15ull ^ (uint64_t)(uintptr_t)__builtin_amdgcn_queue_ptr();
+}
+
+// polls of a wait before it gives up (each ~1-2 us: uncached loads plus a
+// sleep); a wait only ends this way if the dispatch order assumption fails
+constexpr int kSpinMax = 200000;
+// rows per wave of the one-launch kernel, measured at T = 1, E = 128, k = 8,
+// H = 2048, I = 768 (graph-replayed block): down 1 row 12.1 us, 2 rows 11.1,
+// 4 rows 18.1; gate|up 1 row 15.8, 2 rows 11.1, 4 rows 13.7 (two launches: 11.5)
+constexpr int kRpwDc1 = 2, kRpwGu1 = 2;
+
+// every thread of the workgroup: wait until flags[0, n) all hold tag
+__device__ __forceinline__ void wait_flags(const uint64_t* f, int n, uint64_t tag, uint32_t* err) {
+  for (int it = 0;; ++it) {
+    int pend = 0;
+    for (int i = (int)threadIdx.x; i < n; i += 256)
+      pend |= __hip_atomic_load(f + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag;
+    if (!__syncthreads_or(pend)) return;
+    if (it == kSpinMax) {
+      if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(4);  // (1: 12.2 us, 4: 12.3, 10: 12.5 at the block above)
+  }
+}
+
+template <int BITS, int GS, int J, int PER, int RPW, bool XS, bool COH>
+__device__ __forceinline__ void gate_up_body(const MoeDecodeParams& p, int bx, int z, unsigned char* xl) {
   constexpr int PACK = 32 / BITS, WPC = 32 / PACK;  // words per chunk
   constexpr int NP = WPC * (16 / BITS);             // pairs per chunk
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int z = blockIdx.y;  // slot t*k + j
+  // z: slot t*k + j; bx: block of rows of I
   const int t = z / p.k, jz = z - t * p.k;
-  const int r0 = (blockIdx.x * 4 + wave) * RPW;
+  const int r0 = (bx * 4 + wave) * RPW;
   const int C = p.H / 32, G = p.H / GS;
   const int64_t wrow = p.H / PACK;  // words per W row
   // x of the lane's chunks (paired after every load is in flight): XS, the
   // token's row copied once per workgroup into LDS (direct copies)
   uint32_t raw[J][16];
-  extern __shared__ __attribute__((aligned(16))) unsigned char xl[];
   if constexpr (XS) {
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x + (int64_t)t * p.H, (uint32_t)p.H * 2);
     const int xb = p.H >> 3;
@@ -122,7 +179,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p)
   // expert from LDS after the barrier (the routing's VALU work, done by every
   // wave of every workgroup, took ~3.7 us of a 13.9 us block at T = 1)
   int e = 0;
-  const bool writer = blockIdx.x == 0 && jz == 0;
+  const bool writer = bx == 0 && jz == 0;
   if (!XS || wave == 0) {
     int sid;
     if (writer) {
@@ -206,9 +263,20 @@ __global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p)
     }
     const float g = wave_sum(pg), u = wave_sum(pu);
     const int r = r0 + rr;
-    if (lane == 0 && r < p.I)
-      p.act[(int64_t)z * p.I + r] = valid_e ? swiglu_bf16(bf2f(f2bf(g)), bf2f(f2bf(u))) : (uint16_t)0;
+    if (lane == 0 && r < p.I) {
+      const uint16_t a = valid_e ? swiglu_bf16(bf2f(f2bf(g)), bf2f(f2bf(u))) : (uint16_t)0;
+      if constexpr (COH)  // written through to the device's coherence point (read by other XCDs in this launch)
+        __hip_atomic_store(p.act + (int64_t)z * p.I + r, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        p.act[(int64_t)z * p.I + r] = a;
+    }
   }
+}
+
+template <int BITS, int GS, int J, int PER, int RPW, bool XS>
+__global__ __launch_bounds__(256) void moe_gate_up_act_kernel(MoeDecodeParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char xl[];
+  gate_up_body<BITS, GS, J, PER, RPW, XS, false>(p, blockIdx.x, blockIdx.y, xl);
 }
 
 // sum over the LPR lanes of each lane group (butterfly, fixed order)
@@ -219,38 +287,40 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-template <int BITS, int GS, int KE, int P, int RPW>
-__global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p) {
+template <int BITS, int GS, int KE, int P, int RPW, int PER, bool FUSED>
+__device__ __forceinline__ void down_body(const MoeDecodeParams& p, int bx, int t, unsigned char* al) {
   constexpr int PACK = 32 / BITS, WPC = 32 / PACK;
   constexpr int NP = WPC * (16 / BITS);
   constexpr int LPR = 64 / KE;  // lanes per expert row
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int t = blockIdx.y;
-  const int d0 = (blockIdx.x * 4 + wave) * RPW;
+  const int d0 = (bx * 4 + wave) * RPW;  // t: the token, bx: block of rows of H
   const int jx = lane / LPR, sub = lane % LPR;  // expert slot and lane within its row
   const int z = t * KE + jx;
   const int C = p.I / 32, G = p.I / GS;
   const int64_t wrow = p.I / PACK;
   // the token's k activation rows (contiguous) copied once per workgroup into
   // LDS (every wave read all of them from L2 before: 4x the bytes); they are
-  // read back after the barrier
-  extern __shared__ __attribute__((aligned(16))) unsigned char al[];
-  {
-    const int ab = KE * p.I * 2 / 16;  // 16-byte pieces (I % 32 == 0)
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.act + (int64_t)t * KE * p.I, (uint32_t)ab * 16);
-    for (int q0 = 0; q0 < ab; q0 += 256) {
-      const int i = q0 + (int)threadIdx.x;
-      copy16_lds(ra, i < ab ? (uint32_t)i * 16 : kOob, al + (q0 + wave * 64) * 16);
-    }
+  // read back after the barrier.  Two launches: the copies first, then the
+  // expert ids and weights the gate|up kernel wrote (their wait also covers
+  // the wave's copies, issued before them).  One launch: the wave routes the
+  // token itself (the router's arithmetic, as the gate|up role does) and the
+  // copies wait until the token's gate|up workgroups have stored the rows.
+  int e;
+  float wz;
+  if constexpr (!FUSED) {
+    copy_act<KE, 0>(p, t, al, wave);
+    asm volatile("" ::: "memory");  // the id load below stays behind the copies
+    __builtin_amdgcn_sched_barrier(0);
+    e = p.idx[z];
+    wz = p.wts[z];
+  } else {
+    int sid;
+    float w;
+    route_wave<PER>(p.logits + (int64_t)t * p.E, p.E, KE, lane, sid, w);
+    e = __shfl(sid, jx);
+    wz = __shfl(w, jx);
   }
-  asm volatile("" ::: "memory");  // the id load below stays behind the copies
-  __builtin_amdgcn_sched_barrier(0);
-  // the expert id and weight (their wait also covers the wave's copies,
-  // issued before them), then every load of the rows; the barrier publishes
-  // the other waves' copies
-  const int e = p.idx[z];
-  const float wz = p.wts[z];
   const bool valid_e = e >= 0 && e < p.E;
   uint32_t w_[RPW][P][WPC];
   uint16_t s_[RPW][P], b_[RPW][P];
@@ -273,7 +343,14 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p
       }
     }
   }
-  asm volatile("s_barrier" ::: "memory");
+  if constexpr (!FUSED) {
+    asm volatile("s_barrier" ::: "memory");  // the other waves' copies have landed
+  } else {
+    wait_flags(p.flags + (int64_t)t * p.gu_per_token, p.gu_per_token, launch_tag(), p.err);
+    copy_act<KE, 16>(p, t, al, wave);  // (sc1: the rows other XCDs stored)
+    __builtin_amdgcn_s_waitcnt(0);  // (the copies are not tracked by the compiler's waits)
+    __syncthreads();
+  }
   if (d0 >= p.H) return;
   uint32_t raw[P][16];
 #pragma unroll
@@ -311,6 +388,39 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p
     for (int j = 0; j < KE; ++j) pr[j] = __shfl(prod, j * LPR);
     const int d = d0 + rr;
     if (lane == 0 && d < p.H) p.out[(int64_t)t * p.H + d] = f2bf(combine_fold<KE>(pr, KE));
+  }
+}
+
+template <int BITS, int GS, int KE, int P, int RPW>
+__global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeDecodeParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char al[];
+  down_body<BITS, GS, KE, P, RPW, 1, false>(p, blockIdx.x, blockIdx.y, al);
+}
+
+// Both steps in one launch: blocks [0, n_gu) take the gate|up role (every
+// token's), the rest the down role.  A down workgroup routes and issues its
+// weight loads at once, then waits for its token's gate|up flags (bounded
+// wait) before it reads the activations.  Workgroups are dispatched in block
+// order on each XCD, so every gate|up workgroup is resident or done before a
+// down workgroup of the same XCD can hold a slot: the waits always end.
+template <int BITS, int GS, int J, int PER, int KE, int P>
+__global__ __launch_bounds__(256) void moe_one_launch_kernel(MoeDecodeParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char sl[];
+  const int b = blockIdx.x;
+  if (b < p.n_gu) {
+    const int z = b / p.gu_x;
+    gate_up_body<BITS, GS, J, PER, kRpwGu1, true, true>(p, b - z * p.gu_x, z, sl);
+    // the rows were stored write-through (sc1): once every wave's stores have
+    // completed, the workgroup's flag (no L2 write-back: that took ~100 us over
+    // a launch's 3072 waves; flags, not one shared count: same-address atomics
+    // serialize)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(p.flags + b, launch_tag(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    const int b2 = b - p.n_gu;
+    const int t = b2 / p.dc_x;
+    down_body<BITS, GS, KE, P, kRpwDc1, PER, true>(p, b2 - t * p.dc_x, t, sl);
   }
 }
 
@@ -358,6 +468,42 @@ moe_fn pick_dc(int k, int P) {
   }
 }
 
+template <int BITS, int GS, int PER, int KE>
+moe_fn pick_one_p(int J, int P) {
+#define LISAQ_ONE_P(JJ)                                                                  \
+  switch (P) {                                                                           \
+    case 1: return moe_one_launch_kernel<BITS, GS, JJ, PER, KE, 1>;                      \
+    case 2: return moe_one_launch_kernel<BITS, GS, JJ, PER, KE, 2>;                      \
+    case 3: return moe_one_launch_kernel<BITS, GS, JJ, PER, KE, 3>;                      \
+    case 4: return moe_one_launch_kernel<BITS, GS, JJ, PER, KE, 4>;                      \
+    case 6: return moe_one_launch_kernel<BITS, GS, JJ, PER, KE, 6>;                      \
+    case 8: return moe_one_launch_kernel<BITS, GS, JJ, PER, KE, 8>;                      \
+    default: return nullptr;                                                             \
+  }
+  if (J == 1) { LISAQ_ONE_P(1) }
+  if (J == 2) { LISAQ_ONE_P(2) }
+  if (J == 3) { LISAQ_ONE_P(3) }
+  if (J == 4) { LISAQ_ONE_P(4) }
+#undef LISAQ_ONE_P
+  return nullptr;
+}
+
+// (k = 2, 4, 8 only: every instance is a large kernel; other k take two launches)
+template <int BITS, int GS, int PER>
+moe_fn pick_one_k(int J, int k, int P) {
+  switch (k) {
+    case 2: return pick_one_p<BITS, GS, PER, 2>(J, P);
+    case 4: return pick_one_p<BITS, GS, PER, 4>(J, P);
+    case 8: return pick_one_p<BITS, GS, PER, 8>(J, P);
+    default: return nullptr;
+  }
+}
+
+template <int BITS, int GS>
+moe_fn pick_one(int J, int E, int k, int P) {
+  return E <= 128 ? pick_one_k<BITS, GS, 2>(J, k, P) : pick_one_k<BITS, GS, 16>(J, k, P);
+}
+
 template <typename F>
 moe_fn by_format(int bits, int gs, F f) {
   if (bits == 4 && gs == 32) return f(std::integral_constant<int, 4>{}, std::integral_constant<int, 32>{});
@@ -372,6 +518,8 @@ moe_fn by_format(int bits, int gs, F f) {
 int down_passes(int64_t I, int k) { return (int)((I / 32 + 64 / k - 1) / (64 / k)); }
 
 }  // namespace
+
+int64_t moe_decode_flags(int64_t T, int64_t I, int k) { return (I + 4 * kRpwGu1 - 1) / (4 * kRpwGu1) * T * k; }
 
 bool moe_decode_supported(int64_t T, int64_t H, int64_t I, int E, int k, int gs, int bits) {
   if (T < 1 || T > 8 || H % 32 || I % 32 || H > 4 * 64 * 32) return false;
@@ -388,23 +536,40 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, in
                       const uint32_t* gw, const uint16_t* gsc, const uint16_t* gbi, const uint32_t* uw,
                       const uint16_t* usc, const uint16_t* ubi, const uint32_t* dw, const uint16_t* dsc,
                       const uint16_t* dbi, uint16_t* act, uint16_t* out, int64_t T, int64_t H, int64_t I, int E,
-                      int k, int gs, int bits) {
+                      int k, int gs, int bits, uint64_t* flags, uint32_t* err) {
   if (!moe_decode_supported(T, H, I, E, k, gs, bits))
     return set_error(LISAQ_EUNSUPPORTED, "moe decode: T=%lld H=%lld I=%lld k=%d gs=%d bits=%d", (long long)T,
                      (long long)H, (long long)I, k, gs, bits);
   MoeDecodeParams p{x, logits, idx, wts, gw, uw, dw, gsc, gbi, usc, ubi, dsc, dbi, act, out, (int)T, (int)H, (int)I, E, k};
   const int J = (int)((H / 32 + 63) / 64);
   const int P = down_passes(I, k);
+  const int gu_x = (int)((I + 4 * kRpwGu - 1) / (4 * kRpwGu)), dc_x = (int)((H + 4 * kRpwDc - 1) / (4 * kRpwDc));
+  const int alds = (int)((k * I * 2 + 4095) / 4096 * 4096);
+  moe_fn one = flags ? by_format(bits, gs, [&](auto B, auto S) {
+    return pick_one<decltype(B)::value, decltype(S)::value>(J, E, k, P);
+  }) : nullptr;
+  if (one) {
+    p.flags = flags;
+    p.err = err;
+    p.gu_x = (int)((I + 4 * kRpwGu1 - 1) / (4 * kRpwGu1));
+    p.n_gu = p.gu_x * (int)(T * k);
+    p.dc_x = (int)((H + 4 * kRpwDc1 - 1) / (4 * kRpwDc1));
+    p.n_dc = p.dc_x * (int)T;
+    p.gu_per_token = p.gu_x * k;
+    const int lds = alds > xl_bytes((int)H) + 16 ? alds : xl_bytes((int)H) + 16;
+    if (int rc = allow_dyn_lds((const void*)one, lds, "moe_one_launch")) return rc;
+    hipLaunchKernelGGL(one, dim3((unsigned)(p.n_gu + p.n_dc)), dim3(256), lds, st, p);
+    return check_launch("moe_one_launch");
+  }
   moe_fn gu = by_format(bits, gs, [&](auto B, auto S) { return pick_gu<decltype(B)::value, decltype(S)::value>(J, E); });
   moe_fn dc = by_format(bits, gs, [&](auto B, auto S) { return pick_dc<decltype(B)::value, decltype(S)::value>(k, P); });
   if (!gu || !dc) return set_error(LISAQ_EUNSUPPORTED, "moe decode: no kernel for J=%d P=%d k=%d", J, P, k);
   const int xlds = kGuXs ? xl_bytes((int)H) + 16 : 0;
-  hipLaunchKernelGGL(gu, dim3((unsigned)((I + 4 * kRpwGu - 1) / (4 * kRpwGu)), (unsigned)(T * k)), dim3(256), xlds, st, p);
+  hipLaunchKernelGGL(gu, dim3((unsigned)gu_x, (unsigned)(T * k)), dim3(256), xlds, st, p);
   int rc = check_launch("moe_gate_up_act");
   if (rc) return rc;
-  const int alds = (int)((k * I * 2 + 4095) / 4096 * 4096);
   if (int rc2 = allow_dyn_lds((const void*)dc, alds, "moe_down_combine")) return rc2;
-  hipLaunchKernelGGL(dc, dim3((unsigned)((H + 4 * kRpwDc - 1) / (4 * kRpwDc)), (unsigned)T), dim3(256), alds, st, p);
+  hipLaunchKernelGGL(dc, dim3((unsigned)dc_x, (unsigned)T), dim3(256), alds, st, p);
   return check_launch("moe_down_combine");
 }
 

@@ -38,7 +38,8 @@ def workspace(device: torch.device, nbytes: int, kind: str = "linear") -> torch.
 
     ``kind`` "linear" is the quantized-matmul workspace (split-K partials of
     the matmul path), reused by calls ordered on one stream; "moe" is scratch
-    for gather_qmm / moe_forward (tile tables, intermediates).
+    for gather_qmm (tile tables, intermediates); "moe_forward" moe_forward's
+    (intermediates, the decode path's flags and give-up word).
 
     A buffer that is outgrown is replaced but never freed: a HIP graph captured
     earlier still holds its address in its kernel arguments, and freeing it
@@ -373,7 +374,9 @@ def moe_forward(x, logits, gate, up, down, top_k: int, group_size=64, bits=4, re
     idx = torch.empty(T, top_k, dtype=torch.int32, device=x.device)
     wts = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
     lib = _lib.load()
-    ws = workspace(x.device, lib.lisaq_moe_workspace(T, H, I, E, top_k, group_size, bits), "moe")
+    # its own buffer: its first word is the fused decode's give-up flag (zero
+    # unless a wait gave up), which no other op may write
+    ws = workspace(x.device, lib.lisaq_moe_workspace(T, H, I, E, top_k, group_size, bits), "moe_forward")
     _lib.call("lisaq_moe_forward", _stream(x), x.data_ptr(), logits.data_ptr(),
               gw.data_ptr(), gs_.data_ptr(), gb.data_ptr(), uw.data_ptr(), us_.data_ptr(), ub.data_ptr(),
               dw.data_ptr(), ds_.data_ptr(), db.data_ptr(), out.data_ptr(), T, H, I, E, top_k,

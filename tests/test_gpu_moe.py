@@ -298,7 +298,7 @@ def test_moe_fused_decode_vs_generic(dev, force_path, T, E, k, H, I, bits, gs):
     dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
     assert _lib.load().lisaq_moe_decode_supported(T, H, I, E, k, gs, bits) == 1
     outs = {}
-    for fused in ("1", "0"):
+    for fused in ("2", "1", "0"):
         force_path("LISAQ_MOE_FUSED", fused)
         o, idx, w = ops.moe_forward(to_dev_bf16(x, dev), to_dev(lg, dev), dv[0], dv[1], dv[2], k, gs, bits,
                                     return_routing=True)
@@ -307,6 +307,64 @@ def test_moe_fused_decode_vs_generic(dev, force_path, T, E, k, H, I, bits, gs):
 
     assert np.array_equal(outs["1"][1], outs["0"][1]) and np.array_equal(outs["1"][2], outs["0"][2])
     assert_close_bf16(outs["1"][0], bf16_bits_to_f32(outs["0"][0]), what=f"fused vs generic T={T} k={k} bits={bits}")
+    # one launch: the two-launch kernels' arithmetic, bit for bit
+    for a, b in zip(outs["2"], outs["1"]):
+        assert np.array_equal(a, b), f"one launch vs two T={T} k={k} bits={bits}"
+    _assert_sync_clear(dev)
+
+
+def _assert_sync_clear(dev):
+    """No wait of the one-launch decode gave up (the give-up word, first in
+    the MoE workspace, is still zero)."""
+    import torch
+
+    torch.cuda.synchronize()
+    word = ops.workspace(dev, 256, "moe_forward")[:4].view(torch.int32).item()
+    assert word == 0, "a one-launch wait gave up"
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_one_launch_repeated(dev, force_path, T):
+    """Eight one-launch decode calls in a row on one stream, each with new
+    router logits and x (flags of one call must not satisfy the next call's
+    waits), every output bitwise equal to the two-launch path's; then the
+    same eight calls captured in a HIP graph and replayed three times (each
+    replay a new dispatch, so a new tag), every replay checked."""
+    import torch
+
+    E, k, H, I, bits, gs = 64, 8, 1024, 512, 4, 64
+    rng = np.random.default_rng(77 + T)
+    stk = lambda n, kk: tuple(a.reshape(E, n, -1) for a in np_linear(rng, E * n, kk, bits, gs))
+    G, U, D = stk(I, H), stk(I, H), stk(H, I)
+    dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
+    xs = [to_dev_bf16(np_x(rng, T, H), dev) for _ in range(8)]
+    lgs = [to_dev(rng.standard_normal((T, E)).astype(np.float32), dev) for _ in range(8)]
+    run = lambda i: ops.moe_forward(xs[i], lgs[i], dv[0], dv[1], dv[2], k, gs, bits)
+    force_path("LISAQ_MOE_FUSED", "1")
+    ref = [run(i).view(torch.int16).clone() for i in range(8)]
+    force_path("LISAQ_MOE_FUSED", "2")
+    got = [run(i).view(torch.int16).clone() for i in range(8)]
+    for i in range(8):
+        assert torch.equal(got[i], ref[i]), f"call {i}"
+    _assert_sync_clear(dev)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        run(0)  # workspace sized before capture
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [run(i) for i in range(8)]
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i in range(8):
+            assert torch.equal(outs[i].view(torch.int16), ref[i]), f"replay {rep} call {i}"
+        _assert_sync_clear(dev)
 
 
 @pytest.mark.parametrize("T,E,k,H,I", [(600, 64, 8, 128, 64), (300, 1024, 4, 256, 128), (600, 1023, 2, 256, 128),
