@@ -36,8 +36,8 @@ METRIC = "4-bit qmv GB/s (% HBM peak) @M=1; qmm TFLOP/s (% bf16 MFMA peak) @M=20
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload, each
 # scaled by the counter's reading for a 64 MiB device copy (see the profiles/ summaries for the
 # commands and raw counts).
-QMV_TRAFFIC_BYTES = round((24578.2 * 1.9993 + 136.0) * 1024)
-QMM_TRAFFIC_BYTES = round((243682.2 * 1.9993 + 131768.9) * 1024)
+QMV_TRAFFIC_BYTES = round((24576.5 * 1.9993 + 136.0) * 1024)
+QMM_TRAFFIC_BYTES = round((243697.5 * 1.9993 + 131780.5) * 1024)
 QMV_KERNEL = "lisaq::qmvp_kernel<4, 64, 3, 2, 16, 1, false>"
 QMM_KERNEL = "lisaq::qmm_kernel<4, 64, 8, 1, 8, true, false, 3, false, 1>"  # M=2048: 256-row tiles, last round split over K (+ qmm_hybrid_reduce_kernel)
 
