@@ -45,6 +45,7 @@ constexpr int kTileTableMaxExperts = 16384;
 // counts[0..2]: matvec tiles, matmul tiles, overflow/bad-ids flag.
 struct TileTableJob {
   int N, limit, MV, BM, BN, SBM, SBN;
+  int fold;  // runs above MV rows and below the limit: 1 = pieces of <= MV rows in class 0 (no class 1)
   int4* mv_tab[2];
   int mv_cap[2], mv_pad[2], mv_vr[2];
   int4* qmm_tab;

@@ -658,8 +658,9 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
   }
   __syncthreads();
   // per-thread tile counts of its experts: matvec class 0 (runs of at most MV
-  // rows), matvec class 1 (longer runs below the limit), matmul, short matmul
-  // (a run's last tile of at most SBM rows; SBM = 0: none)
+  // rows; with fold also the longer runs below the limit, in pieces of MV),
+  // matvec class 1 (longer runs below the limit), matmul, short matmul (a
+  // run's last tile of at most SBM rows; SBM = 0: none)
   const int SBM = job.qs_tab ? job.SBM : 0;
   const int nv0 = (N + job.mv_vr[0] - 1) / job.mv_vr[0];
   const int nv1 = (N + job.mv_vr[1] - 1) / job.mv_vr[1];
@@ -677,6 +678,7 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
       c[2] += (len / BM + (rem > 0 && !sh ? 1 : 0)) * ntbn;
       c[3] += sh ? ntsb : 0;
     } else if (len <= MV) c[0] += nv0;
+    else if (job.fold) c[0] += nv0 * ((len + MV - 1) / MV);
     else c[1] += nv1;
   }
   // inclusive scan of the per-thread counts: within each wave by shuffles,
@@ -727,9 +729,14 @@ __global__ __launch_bounds__(1024) void tile_table_kernel(const int32_t* __restr
           for (int nt = 0; nt < (sh ? ntsb : ntbn); ++nt, ++oq)
             if (oq < caps[sh ? 3 : 2]) tab[oq] = make_int4(e, st + r0, rows, nt);
         }
-      } else if (len <= MV) {
-        for (int nt = 0; nt < nv0; ++nt, ++o[0])
-          if (o[0] < caps[0]) job.mv_tab[0][o[0]] = make_int4(e, st, len, nt);
+      } else if (len <= MV || job.fold) {
+        // (fold: a longer run as pieces of at most MV rows; a row's arithmetic
+        // does not depend on the tile it runs in)
+        for (int r0 = 0; r0 < len; r0 += MV) {
+          const int rows = len - r0 < MV ? len - r0 : MV;
+          for (int nt = 0; nt < nv0; ++nt, ++o[0])
+            if (o[0] < caps[0]) job.mv_tab[0][o[0]] = make_int4(e, st + r0, rows, nt);
+        }
       } else {
         for (int nt = 0; nt < nv1; ++nt, ++o[1])
           if (o[1] < caps[1]) job.mv_tab[1][o[1]] = make_int4(e, st, len, nt);

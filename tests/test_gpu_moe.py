@@ -153,6 +153,25 @@ def test_gather_qmm_walking_grid(dev, oracle, force_path, kernel):
     assert_close_bf16(from_dev_bf16(y), ref, what=f"gather walking grid [{kernel}]")
 
 
+@pytest.mark.parametrize("N,K", [(768, 2048), (2048, 768)])
+def test_gather_qmm_folded_runs(dev, oracle, N, K):
+    """Short runs on average (at most 8 rows: the tile tables put runs longer than the 16-row matvec
+    class in pieces of 16 rows into that class, with no launch for the longer class) with runs of 17,
+    25 and 32 rows among them, and one run at the matvec limit (matmul arithmetic)."""
+    E = 40
+    limit = ops.qmv_batch_limit(K, N)
+    rng = np.random.default_rng(N + K)
+    W, S, B = _expert_stack(rng, E, N, K)
+    lens = [int(v) for v in rng.integers(1, 4, E - 4)] + [17, 25, 32, limit]
+    assert sum(lens) <= 8 * E and max(lens[:-1]) < limit
+    ids = np.concatenate([np.full(n, e, np.int32) for e, n in enumerate(lens)])
+    x = np_x(rng, ids.size, K)
+    y = ops.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(W, dev), to_dev_bf16(S, dev), to_dev_bf16(B, dev),
+                       rhs_indices=to_dev(ids, dev), group_size=64, bits=4)
+    ref = _gather_ref(oracle, x, W, S, B, ids, limit)
+    assert_close_bf16(from_dev_bf16(y), ref, what=f"gather folded runs N={N} K={K}")
+
+
 @pytest.mark.parametrize("T", [1, 4, 64])
 def test_moe_forward_parity(dev, oracle, T):
     """Whole routed SwitchGLU vs the oracle chain, with the reference shapes
