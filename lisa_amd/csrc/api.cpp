@@ -287,8 +287,12 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   const bool mm = mr >= L.limit;
   const bool short_ok = mm && L.mc.BM > kShortBM && path_int("LISAQ_GATHER_SHORT", 1) != 0;
   const int64_t ntbn = (N + L.mc.BN - 1) / L.mc.BN;
-  L.qmm_cap = (mm && !(short_ok && mr <= kShortBM)) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs) * ntbn) : 0;
-  L.qs_cap = short_ok ? (int)(runs * ((N + L.short_bn() - 1) / L.short_bn())) : 0;
+  // runs that can reach the limit: at most R / limit of them (the matmul
+  // grids are sized by it: MoE T = 64, where such runs are rare, launched 768
+  // and 1024 short-tile workgroups that found no tile)
+  const int64_t runs_mm = runs < R / L.limit ? runs : R / L.limit;
+  L.qmm_cap = (mm && !(short_ok && mr <= kShortBM)) ? (int)(((R + L.mc.BM - 1) / L.mc.BM + runs_mm) * ntbn) : 0;
+  L.qs_cap = short_ok ? (int)(runs_mm * ((N + L.short_bn() - 1) / L.short_bn())) : 0;
   L.qmm_off = o;
   L.qs_off = L.qmm_off + up256((size_t)L.qmm_cap * 16);
   L.total = L.qs_off + up256((size_t)L.qs_cap * 16);
