@@ -194,7 +194,8 @@ struct GatherLayout {
 
 static size_t up256(size_t v) { return (v + 255) / 256 * 256; }
 
-// Rows of x of the short-run matvec class (runs up to this length)
+// Rows of x of the short-run matvec class (runs up to this length; half of
+// it when runs average at most 4 rows)
 constexpr int kGatherMvRows = 16;
 
 // max_run: an upper bound of the longest run of equal ids when the caller
@@ -216,7 +217,10 @@ static GatherLayout gather_layout(int64_t R, int64_t N, int64_t K, int E, int gs
   L.Mmax = (int)((mr < L.limit - 1) ? mr : L.limit - 1);
   if (L.Mmax < 1) L.Mmax = 1;
   const int64_t avg = R / (runs > 0 ? runs : 1);  // average run length
-  int mv = tune_int("LISAQ_GATHER_MV_ROWS", kGatherMvRows);
+  // (runs averaging at most 4 rows: 8-row tiles, less x staged per tile;
+  // measured at E = 128, k = 8: T = 16 73 -> 69 us, T = 32 91 -> 87 us, T = 64
+  // 111 -> 108 us; at T = 128, 8 rows on average, 124 -> 146 us)
+  int mv = tune_int("LISAQ_GATHER_MV_ROWS", avg <= 4 ? kGatherMvRows / 2 : kGatherMvRows);
   if (mv < 1) mv = 1;
   // runs averaging at least half the limit leave few runs to the matvec: one
   // class (one launch) then, sized for the limit (a row's arithmetic does not

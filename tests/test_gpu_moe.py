@@ -155,9 +155,9 @@ def test_gather_qmm_walking_grid(dev, oracle, force_path, kernel):
 
 @pytest.mark.parametrize("N,K", [(768, 2048), (2048, 768)])
 def test_gather_qmm_folded_runs(dev, oracle, N, K):
-    """Short runs on average (at most 8 rows: the tile tables put runs longer than the 16-row matvec
-    class in pieces of 16 rows into that class, with no launch for the longer class) with runs of 17,
-    25 and 32 rows among them, and one run at the matvec limit (matmul arithmetic)."""
+    """Short runs on average (4 rows here: the tile tables use the 8-row matvec class and put longer
+    runs below the limit in pieces of 8 rows into it, with no launch for a longer class) with runs of
+    17, 25 and 32 rows among them, and one run at the matvec limit (matmul arithmetic)."""
     E = 40
     limit = ops.qmv_batch_limit(K, N)
     rng = np.random.default_rng(N + K)
