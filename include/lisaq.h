@@ -243,8 +243,8 @@ LISAQ_API int lisaq_moe_combine(void* stream, const void* down_sorted, const flo
  * topk_idx/topk_weights [T,k] may be NULL.
  * Few tokens (lisaq_moe_decode_supported: T <= 8, the engine's decode window,
  * moe.rs:263-332, 415-420) take the fused decode path of moe_decode.rs
- * (routing + gate|up + SwiGLU, then down + combine, in one launch whose
- * down workgroups wait for their token's gate|up workgroups' flags), with the same
+ * (routing + gate|up + SwiGLU, then down + combine; for one token in one
+ * launch whose down workgroups wait for the gate|up workgroups' flags), with the same
  * rounding points; the path override LISAQ_MOE_FUSED (lisaq_set_path_override)
  * 1 selects two launches (the same arithmetic), 0 the generic path.  Many
  * tokens (T*k >= 20*E, H % 64 == 0, I % 64 == 0) take

@@ -1,5 +1,5 @@
 // Fused decode MoE (few tokens): gate|up matvec + SwiGLU and down matvec +
-// weighted combine, routing inside, in one launch (k = 2, 4, 8) or two.
+// weighted combine, routing inside, in one launch (T = 1, k = 2, 4, 8) or two.
 //
 // Reference: the engine's one-token decode MoE, track_moe_route_1 ->
 // track_moe_gate_up_reuse_2row -> track_moe_down_combine_1
@@ -545,7 +545,11 @@ int launch_moe_decode(hipStream_t st, const uint16_t* x, const float* logits, in
   const int P = down_passes(I, k);
   const int gu_x = (int)((I + 4 * kRpwGu - 1) / (4 * kRpwGu)), dc_x = (int)((H + 4 * kRpwDc - 1) / (4 * kRpwDc));
   const int alds = (int)((k * I * 2 + 4095) / 4096 * 4096);
-  moe_fn one = flags ? by_format(bits, gs, [&](auto B, auto S) {
+  // one launch for one token only (measured at E = 128, k = 8, one vs two
+  // launches: T = 1 10.9 vs 11.6 us, T = 2 18.4 vs 15.7, T = 4 30.7 vs 27.4,
+  // T = 8 57.0 vs 47.8: with more tokens the waiting down workgroups hold
+  // slots the gate|up workgroups need)
+  moe_fn one = flags && T == 1 ? by_format(bits, gs, [&](auto B, auto S) {
     return pick_one<decltype(B)::value, decltype(S)::value>(J, E, k, P);
   }) : nullptr;
   if (one) {

@@ -342,17 +342,18 @@ def _assert_sync_clear(dev):
     assert word == 0, "a one-launch wait gave up"
 
 
-@pytest.mark.parametrize("T", [1, 4])
-def test_moe_one_launch_repeated(dev, force_path, T):
-    """Eight one-launch decode calls in a row on one stream, each with new
-    router logits and x (flags of one call must not satisfy the next call's
-    waits), every output bitwise equal to the two-launch path's; then the
+@pytest.mark.parametrize("T,k", [(1, 8), (1, 4), (1, 2), (4, 8)])
+def test_moe_one_launch_repeated(dev, force_path, T, k):
+    """Eight one-launch decode calls in a row on one stream (T = 1; T = 4
+    takes two launches either way), each with new router logits and x (flags
+    of one call must not satisfy the next call's waits), every output bitwise
+    equal to the two-launch path's; then the
     same eight calls captured in a HIP graph and replayed three times (each
     replay a new dispatch, so a new tag), every replay checked."""
     import torch
 
-    E, k, H, I, bits, gs = 64, 8, 1024, 512, 4, 64
-    rng = np.random.default_rng(77 + T)
+    E, H, I, bits, gs = 64, 1024, 512, 4, 64
+    rng = np.random.default_rng(77 + T + k)
     stk = lambda n, kk: tuple(a.reshape(E, n, -1) for a in np_linear(rng, E * n, kk, bits, gs))
     G, U, D = stk(I, H), stk(I, H), stk(H, I)
     dv = [tuple(to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev) for i, a in enumerate(st)) for st in (G, U, D)]
