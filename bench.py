@@ -7,7 +7,10 @@ step is one quantized_matmul call on one of 8 distinct weight sets used in
 rotation (8 x 50.2 MB = 401 MB > the 256 MB Infinity Cache), so weights
 stream from HBM.  Inputs are resident in HBM before the timed region; the K
 timed steps are replayed from a HIP graph so host launch overhead is not
-timed.  The qmm figure (M=2048, TFLOP/s of 2*M*N*K) is reported beside it.
+timed, and the device's own clock, stored by a one-lane launch inside the
+graph before the first and after the last step, times them (the hipEvent
+bracket around the replay, which also holds the replay's start-up on the
+device, is reported beside it as ``event_ms_per_step``).  The qmm figure (M=2048, TFLOP/s of 2*M*N*K) is reported beside it.
 
 ``cpu_baseline`` times the CPU oracle's fused dequant-dot (the reference's
 dequantize-then-matmul arithmetic, oracle/lisaq_oracle.c) on the host cores
@@ -124,11 +127,24 @@ def main():
             step(i)
     stream.synchronize()
 
-    def capture(n):
+    from lisa_amd import _lib
+
+    lib = _lib.load()
+    stamps = torch.zeros(2, dtype=torch.int64, device=dev)
+
+    def capture(n, stamped=False):
+        # stamped: the GPU's 100 MHz clock stored right before the first and
+        # right after the last step, inside the graph (the replay's start on
+        # the device, a few us per replay, stays outside; it is in the event
+        # bracket, reported beside)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
+            if stamped:
+                _lib.check(lib.lisaq_timestamp(stream.cuda_stream, stamps.data_ptr()))
             for i in range(n):
                 step(i)
+            if stamped:
+                _lib.check(lib.lisaq_timestamp(stream.cuda_stream, stamps.data_ptr() + 8))
         return g
 
     # W untimed warm-up steps, replayed from a graph like the timed ones, then
@@ -136,7 +152,7 @@ def main():
     # CLOCK_WARM_S (it reaches its steady clock after ~20 ms of sustained load;
     # a handful of calls is ~0.1 ms and leaves it ramping)
     g_warm = capture(max(args.warmup, 1))
-    g_timed = capture(args.steps)
+    g_timed = capture(args.steps, stamped=True)
     t_w = time.perf_counter()
     warm_replays = 0
     while warm_replays < 1 or time.perf_counter() - t_w < CLOCK_WARM_S:
@@ -155,7 +171,9 @@ def main():
         e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = e0.elapsed_time(e1)
+    event_ms = e0.elapsed_time(e1)
+    t_stamp = stamps.cpu().tolist()
+    gpu_ms = (t_stamp[1] - t_stamp[0]) * 1e-5  # 100 MHz ticks
     per_step_s = gpu_ms * 1e-3 / args.steps
     nbytes = qmv_bytes(M, N, K, bits, gs)
     gbs = nbytes / per_step_s / 1e9
@@ -197,8 +215,10 @@ def main():
             "workload": "qmv 4-bit gs64 M=1 K=5120 N=17408 (decode matvec), 8 rotating weight sets",
             "bits": bits, "group_size": gs, "M": M, "K": K, "N": N, "weight_sets": len(sets),
             "bytes_per_step": nbytes,
-            "timing": f"HIP graph replay of the timed steps, hipEvent bracket, after the W warm-up steps and "
+            "timing": f"HIP graph replay of the timed steps, device clock (lisaq_timestamp) stored inside the "
+                      f"graph before the first and after the last step, after the W warm-up steps and "
                       f"{warm_replays} replays of them ({CLOCK_WARM_S * 1e3:.0f} ms of clock warm-up)",
+            "event_ms_per_step": round(event_ms / args.steps, 5),
             "wall_s": round(wall, 4),
         },
         "roofline": {
@@ -223,8 +243,15 @@ def main():
 def _time_graph(stream, fn, n_sets, steps, warm_s=CLOCK_WARM_S):
     """Average seconds per call of fn(i) over `steps` calls replayed from a HIP graph (i cycles
     over n_sets inputs), after untimed replays of the same graph for at least `warm_s` seconds
-    (steady clock; the first replays of a new graph over new buffers run slow)."""
+    (steady clock; the first replays of a new graph over new buffers run slow).  Timed by the
+    device clock stored inside the graph before the first and after the last call
+    (lisaq_timestamp), as the headline."""
     import torch
+
+    from lisa_amd import _lib
+
+    lib = _lib.load()
+    stamps = torch.zeros(2, dtype=torch.int64, device=stream.device)
 
     # inputs were made on the current stream; the calls below share library
     # workspaces with any eager call still queued there
@@ -235,8 +262,10 @@ def _time_graph(stream, fn, n_sets, steps, warm_s=CLOCK_WARM_S):
     stream.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
+        _lib.check(lib.lisaq_timestamp(stream.cuda_stream, stamps.data_ptr()))
         for i in range(steps):
             fn(i)
+        _lib.check(lib.lisaq_timestamp(stream.cuda_stream, stamps.data_ptr() + 8))
     t0 = time.perf_counter()
     reps = 0
     while reps < 2 or time.perf_counter() - t0 < warm_s:
@@ -244,15 +273,12 @@ def _time_graph(stream, fn, n_sets, steps, warm_s=CLOCK_WARM_S):
             g.replay()
         torch.cuda.synchronize()
         reps += 1
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        e0.record(stream)
         g.replay()
-        e1.record(stream)
     torch.cuda.synchronize()
     del g
-    return e0.elapsed_time(e1) * 1e-3 / steps
+    t = stamps.cpu().tolist()
+    return (t[1] - t[0]) * 1e-8 / steps  # 100 MHz ticks
 
 
 def read_floor(dev):

@@ -74,6 +74,12 @@ LISAQ_API const char* lisaq_last_error(void);
  * a guard the loads feed, never stored in practice).  The floor a kernel
  * reading the same bytes can reach, timed by bench.py --read-floor. */
 LISAQ_API int lisaq_read_stream(void* stream, const void* src, size_t bytes, int loads_per_lane, uint32_t* sink);
+/* Measurement aid, no counterpart in the reference: enqueue one tiny launch
+ * that stores the GPU's constant 100 MHz clock (s_memrealtime) into *dst
+ * (device memory, 8-byte aligned) when it runs.  Two of them around a run of
+ * launches on one stream (also inside a captured graph) give the device time
+ * of that run without the host's submission of it. */
+LISAQ_API int lisaq_timestamp(void* stream, uint64_t* dst);
 
 #define LISAQ_PATH_DEFAULT (-2147483647 - 1)
 LISAQ_API int lisaq_set_path_override(const char* name, int value);

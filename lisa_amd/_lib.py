@@ -45,6 +45,7 @@ SIGNATURES = {
     "lisaq_last_error": (ctypes.c_char_p, []),
     "lisaq_set_path_override": (ci, [ctypes.c_char_p, ci]),
     "lisaq_read_stream": (ci, [vp, vp, sz, ci, vp]),
+    "lisaq_timestamp": (ci, [vp, vp]),
     "lisaq_quantized_matmul": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci, vp, sz]),
     "lisaq_quantized_matmul_workspace": (sz, [i64, i64, i64, ci, ci]),
     "lisaq_quantized_matmul_noalloc": (ci, [vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, ci, ci]),

@@ -490,6 +490,12 @@ int lisaq_read_stream(void* stream, const void* src, size_t bytes, int loads_per
   return launch_read_stream((hipStream_t)stream, src, bytes, loads_per_lane, sink);
 }
 
+int lisaq_timestamp(void* stream, uint64_t* dst) {
+  g_err[0] = 0;
+  LISAQ_REQUIRE(dst && aligned(dst, 8), LISAQ_EINVAL_LAYOUT, "timestamp: null or unaligned destination");
+  return launch_timestamp((hipStream_t)stream, dst);
+}
+
 int lisaq_set_path_override(const char* name, int value) {
   const int i = lisaq::path_slot(name);
   LISAQ_REQUIRE(i >= 0, LISAQ_EINVAL_SHAPE, "set_path_override: unknown path %s", name ? name : "(null)");

@@ -45,4 +45,18 @@ int launch_read_stream(hipStream_t st, const void* src, size_t bytes, int loads_
   return check_launch("read_stream");
 }
 
+// The GPU's constant 100 MHz clock (s_memrealtime), stored by one lane:
+// stream-ordered, so two of them around a run of kernels time that run on the
+// device, without the host's submission of it (bench.py brackets the timed
+// graph's steps with them inside the graph).
+__global__ __launch_bounds__(64) void timestamp_kernel(uint64_t* dst) {
+  const uint64_t t = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) dst[0] = t;
+}
+
+int launch_timestamp(hipStream_t st, uint64_t* dst) {
+  hipLaunchKernelGGL(timestamp_kernel, dim3(1), dim3(64), 0, st, dst);
+  return check_launch("timestamp");
+}
+
 }  // namespace lisaq

@@ -65,5 +65,7 @@ int launch_sort_parallel(hipStream_t st, const int32_t* ids, int64_t R, int E, i
 
 // measurement aid: read `bytes` of src (16-byte lanes, loads_per_lane 1 KB pieces per wave)
 int launch_read_stream(hipStream_t st, const void* src, size_t bytes, int loads_per_lane, uint32_t* sink);
+// measurement aid: *dst = the GPU's 100 MHz clock when the launch runs
+int launch_timestamp(hipStream_t st, uint64_t* dst);
 
 }  // namespace lisaq
