@@ -36,6 +36,7 @@
 #include "kernels.h"
 #include "moe_dev.h"
 #include "qmv_dev.h"
+#include "sync_dev.h"
 
 namespace lisaq {
 using namespace qmvdev;
@@ -108,37 +109,12 @@ __device__ __forceinline__ void copy_act(const MoeDecodeParams& p, int t, unsign
 
 // One launch: gate|up workgroup b stores this launch's tag in flags[b] once
 // its rows are stored; a down workgroup waits until every flag of its token
-// holds the tag.  The tag is unique per dispatch (the packet's dispatch id
-// on its queue, mixed with the queue's address), so flags left by earlier
-// launches never match and nothing is ever reset.
-extern "C" __device__ uint64_t lisaq_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+// holds the tag (sync_dev.h).
 
-__device__ __forceinline__ uint64_t launch_tag() {
-  return lisaq_dispatch_id() * 0x9E3779B97F4A7C15ull ^ (uint64_t)(uintptr_t)__builtin_amdgcn_queue_ptr();
-}
-
-// polls of a wait before it gives up (each ~1-2 us: uncached loads plus a
-// sleep); a wait only ends this way if the dispatch order assumption fails
-constexpr int kSpinMax = 200000;
 // rows per wave of the one-launch kernel, measured at T = 1, E = 128, k = 8,
 // H = 2048, I = 768 (graph-replayed block): down 1 row 12.1 us, 2 rows 11.1,
 // 4 rows 18.1; gate|up 1 row 15.8, 2 rows 11.1, 4 rows 13.7 (two launches: 11.5)
 constexpr int kRpwDc1 = 2, kRpwGu1 = 2;
-
-// every thread of the workgroup: wait until flags[0, n) all hold tag
-__device__ __forceinline__ void wait_flags(const uint64_t* f, int n, uint64_t tag, uint32_t* err) {
-  for (int it = 0;; ++it) {
-    int pend = 0;
-    for (int i = (int)threadIdx.x; i < n; i += 256)
-      pend |= __hip_atomic_load(f + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag;
-    if (!__syncthreads_or(pend)) return;
-    if (it == kSpinMax) {
-      if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    __builtin_amdgcn_s_sleep(4);  // (1: 12.2 us, 4: 12.3, 10: 12.5 at the block above)
-  }
-}
 
 template <int BITS, int GS, int J, int PER, int RPW, bool XS, bool COH>
 __device__ __forceinline__ void gate_up_body(const MoeDecodeParams& p, int bx, int z, unsigned char* xl) {
@@ -347,7 +323,7 @@ __device__ __forceinline__ void down_body(const MoeDecodeParams& p, int bx, int 
     asm volatile("s_barrier" ::: "memory");  // the other waves' copies have landed
   } else {
     wait_flags(p.flags + (int64_t)t * p.gu_per_token, p.gu_per_token, launch_tag(), p.err);
-    copy_act<KE, 16>(p, t, al, wave);  // (sc1: the rows other XCDs stored)
+    copy_act<KE, kSc1>(p, t, al, wave);  // (sc1: the rows other XCDs stored)
     __builtin_amdgcn_s_waitcnt(0);  // (the copies are not tracked by the compiler's waits)
     __syncthreads();
   }
@@ -416,7 +392,7 @@ __global__ __launch_bounds__(256) void moe_one_launch_kernel(MoeDecodeParams p) 
     // serialize)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(p.flags + b, launch_tag(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) store_flag(p.flags + b, launch_tag());
   } else {
     const int b2 = b - p.n_gu;
     const int t = b2 / p.dc_x;
