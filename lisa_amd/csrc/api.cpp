@@ -44,10 +44,11 @@ int tune_int(const char* name, int dflt) {
 // the environment), so a serving process runs the dispatcher's choice unless
 // its own code asks otherwise.  kPathNone = unset.
 static const char* const kPathNames[] = {"LISAQ_QMV_KERNEL", "LISAQ_QMM_SPLIT", "LISAQ_GATHER_SHORT",
-                                         "LISAQ_MOE_GU", "LISAQ_MOE_FUSED", "LISAQ_MOE_GU_MV"};
+                                         "LISAQ_MOE_GU",     "LISAQ_MOE_FUSED", "LISAQ_MOE_GU_MV",
+                                         "LISAQ_SERIAL_ROWS"};
 static constexpr int kPathNone = INT32_MIN;
 static constexpr int kNumPaths = (int)(sizeof(kPathNames) / sizeof(kPathNames[0]));
-static std::atomic<int> g_path[kNumPaths] = {{kPathNone}, {kPathNone}, {kPathNone},
+static std::atomic<int> g_path[kNumPaths] = {{kPathNone}, {kPathNone}, {kPathNone}, {kPathNone},
                                              {kPathNone}, {kPathNone}, {kPathNone}};
 
 static int path_slot(const char* name) {
@@ -649,25 +650,42 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
   // The M=1 schedule (same slabs, same waves) applied to every row gives each
   // row the arithmetic of an independent M=1 call.
   const QmvConfig c = qmv_config(1, N, K, gs, bits);
-  if (c.kind == 5) {
-    // one weight stream for all rows; every row's arithmetic is the one-row
-    // kernel's (the row split of the matrix cores never mixes rows of x)
-    const QmvConfig cw = qmv_config(M, N, K, gs, bits);
-    if (cw.kind == 5)
-      return run_qmv((hipStream_t)stream, cw, x, w, s, b, y, M, N, K, gs, bits, ws, ws_bytes);
-    // staged x too large for all rows at once: two halves, each bitwise the same per row
-    const int64_t h = (M + 1) / 2;
-    const QmvConfig c1 = qmv_config(h, N, K, gs, bits), c2 = qmv_config(M - h, N, K, gs, bits);
-    if (c1.kind != 5 || c2.kind != 5) return set_error(LISAQ_EUNSUPPORTED, "serial_rows: no one-stream configuration");
-    rc = run_qmv((hipStream_t)stream, c1, x, w, s, b, y, h, N, K, gs, bits, ws, ws_bytes);
-    if (rc) return rc;
-    return run_qmv((hipStream_t)stream, c2, (const uint16_t*)x + h * K, w, s, b, (uint16_t*)y + h * N, M - h, N, K,
-                   gs, bits, ws, ws_bytes);
+  // Eight or four rows at a time on one weight stream with the one-row
+  // kernels' arithmetic (the persistent and wave-rows kernels give every row
+  // the same bits; eight where eight staged rows of x fit the LDS); the rows
+  // left (at most three) go the pair way below.  Measured (4-bit, cold,
+  // graph-replayed, these rows vs pairs): 2560 x 9728 4 rows 12.1 vs 17.3 us,
+  // 8 rows (two fours) 24.2 vs 34.2; 9728 x 2560 4 rows 13.4 vs 14.7, 8 rows
+  // 21.2 vs 29.0; the north-star shape 4 rows 26.8 vs 26.7, 8 rows 51.4 vs
+  // 53.0 (the dot products of eight rows bound it: VALU issue).  Three rows in
+  // a four-row launch lose to a pair and a single (26.9 vs 23.8 there).
+  int64_t r_done = 0;
+  if ((c.kind == 4 || c.kind == 6) && path_int("LISAQ_SERIAL_ROWS", 1) != 0) {
+    while (M - r_done >= 4) {
+      const int64_t left = M - r_done;
+      int64_t mr = 0;
+      if (left >= 8 && qmvs_rows_supported(8, N, K, gs, bits)) mr = 8;
+      else if (qmvs_rows_supported(4, N, K, gs, bits)) mr = 4;
+      if (!mr) break;
+      QmvParams p{};
+      p.x = (const uint16_t*)x + r_done * K;
+      p.w = w;
+      p.s = (const uint16_t*)s;
+      p.b = (const uint16_t*)b;
+      p.y = (uint16_t*)y + r_done * N;
+      p.M = (int)mr;
+      p.N = (int)N;
+      p.K = (int)K;
+      p.G = (int)(K / gs);
+      if ((rc = qmvs_rows_launch((hipStream_t)stream, p, bits))) return rc;
+      r_done += mr;
+    }
+    if (r_done == M) return LISAQ_OK;
   }
   if (c.kind == 4) {
     // the persistent kernel computes each of its (one or two) rows with the
     // one-row arithmetic, so pairs of rows share one pass over W
-    for (int64_t r = 0; r < M; r += 2) {
+    for (int64_t r = r_done; r < M; r += 2) {
       const int64_t mr = M - r < 2 ? M - r : 2;
       const QmvConfig cp = mr == 1 ? c : qmvp_config(2, N, K, gs, bits);
       if (cp.kind != 4) return set_error(LISAQ_EUNSUPPORTED, "serial_rows: no two-row persistent kernel");
@@ -681,7 +699,7 @@ int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32
     // the wave-rows kernel's arithmetic is the persistent kernel's: pairs of
     // rows share one pass over W (in either kernel); rows one at a time where
     // no two-row configuration exists (long rows)
-    for (int64_t r = 0; r < M; r += 2) {
+    for (int64_t r = r_done; r < M; r += 2) {
       const int64_t mr = M - r < 2 ? M - r : 2;
       QmvConfig cp = mr == 1 ? c : qmvs_config(2, N, K, gs, bits);
       if (cp.kind != 6 && mr == 2) cp = qmvp_config(2, N, K, gs, bits);

@@ -105,6 +105,11 @@ int qmvp_addnorm_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int
 QmvConfig qmvs_config(int64_t M, int64_t N, int64_t K, int gs, int bits, bool addnorm = false);
 int qmvs_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs);
 int qmvs_addnorm_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs);
+// up to 8 rows of x (run as four or eight: rows past M read as zero) on one
+// weight stream, every row bitwise the one-row kernels' row (gs 64; plain
+// rows; p.x, p.w, p.s, p.b, p.y, p.M, p.N, p.K set)
+bool qmvs_rows_supported(int64_t M, int64_t N, int64_t K, int gs, int bits);
+int qmvs_rows_launch(hipStream_t stream, QmvParams p, int bits);
 
 // Enqueue; grid_x = number of row tiles (or tile-table entries).
 int qmv_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs, int grid_x);

@@ -274,6 +274,210 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Verify rows: MR rows of x (3..8; rows past M read as zero and are not
+// stored) on one weight stream, every row with exactly the one-row arithmetic
+// above (lane l, chunks l, l+64, ..., the same fused multiply-adds in the same
+// order, the same 64-lane DPP sum), so each row is bitwise the row of a
+// one-row call (jit::affine_verify_qmm's contract, crates/lisa-mlx/src/jit/
+// matmul.rs:579-664).  With MR rows the lane's paired x of every pass would
+// not fit the registers (MR x J x 16), so the loop runs pass-major: x is
+// copied into LDS as in the kernel above, the workgroup pairs it in place
+// (the pairs of a chunk are a permutation of its 16 words) with the chunks'
+// sums beside, and for pass j each wave reads the pairs of its lanes' chunk j,
+// four rows of x at a time, then runs that chunk of all its RW rows of W,
+// carrying RW x MR partial chains in registers; each chain's order is
+// unchanged.
+__host__ __device__ static inline int qmvs_rows_xs_bytes(int MR, int C) { return MR * C * 16; }
+// eight waves per workgroup: the staged rows of x (80 KB for eight rows at
+// K = 5120) are shared by twice the rows of W, and a compute unit still holds
+// eight waves when one workgroup is all its LDS allows
+constexpr int kRowsWaves = 8;
+__host__ __device__ static inline int qmvs_rows_x_region(int MR, int K) {
+  return ((MR * K * 2 + 16 * 64 * kRowsWaves - 1) / (16 * 64 * kRowsWaves)) * (16 * 64 * kRowsWaves);
+}
+
+template <int BITS, int J, int RW, int MR>
+__global__ __launch_bounds__(64 * kRowsWaves) void qmvs_rows_kernel(QmvParams p) {
+  constexpr int GS = 64;
+  constexpr int CB = BITS == 4 ? 16 : 8;
+  constexpr int WPC = CB / 4;
+  constexpr int PPW = 16 / BITS;
+  constexpr int NP = WPC * PPW;
+  constexpr int MH = 4;  // rows of x per step inside a pass
+  static_assert(MR % MH == 0, "rows of x in fours");
+  typedef uint32_t chunk_t __attribute__((ext_vector_type(WPC)));
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int N = p.N, K = p.K, C = p.chunks, G = p.G, M = p.M;
+  const uint32_t rowbytes = (uint32_t)C * CB;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int xreg = qmvs_rows_x_region(MR, K), xsreg = (qmvs_rows_xs_bytes(MR, C) + 15) / 16 * 16;
+  const int sreg = qmvs_sb_region(RW, G);
+  unsigned char* xL = lds;                                // x, then its pairs in place (x_slot layout)
+  float* xsL = reinterpret_cast<float*>(lds + xreg);      // [MR][C][4] sums
+  unsigned char* sL = lds + xreg + xsreg + wave * 2 * sreg;
+  unsigned char* bL = sL + sreg;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2);  // (rows past M read as zero)
+
+  // --- 1. the MR rows of x (LDS copies), paired in place once per workgroup
+  // (the one-row kernel's pairing and sums): the workgroup then walks blocks
+  // of rows of W (a grid stride), so x is staged once per workgroup, not once
+  // per block
+  {
+    const int xb = (K * 2 * MR) >> 4;
+    for (int q0 = 0; q0 < xb; q0 += 64 * kRowsWaves) {  // (uniform)
+      const int i = q0 + t;
+      const int pc = x_piece(i);
+      copy16(rx, pc < xb ? (uint32_t)pc * 16 : kOob, xL + (q0 + wave * 64) * 16);
+    }
+  }
+  wait_vm<0>();
+  lds_sync();
+  for (int it = t; it < MR * C; it += 64 * kRowsWaves) {
+    const int m = it / C, c = it - m * C;
+    uint32_t raw[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(xL + x_slot(m * (K >> 3) + 4 * c + i) * 16);
+      raw[4 * i] = v[0];
+      raw[4 * i + 1] = v[1];
+      raw[4 * i + 2] = v[2];
+      raw[4 * i + 3] = v[3];
+    }
+    uint32_t xp[NP];
+    XSums xs;
+    pair_x<BITS>(raw, xp, xs);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4*>(xL + x_slot(m * (K >> 3) + 4 * c + i) * 16) =
+          u32x4{xp[4 * i], xp[4 * i + 1], xp[4 * i + 2], xp[4 * i + 3]};
+    *reinterpret_cast<f32x4*>(xsL + it * 4) = f32x4{xs.t[0], xs.t[1], xs.t[2], xs.sx};
+  }
+  lds_sync();
+
+  PConst kc;
+  kc.init();
+  const int nblk = (N + RW * kRowsWaves - 1) / (RW * kRowsWaves);
+  for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x) {  // (uniform)
+    const int r0 = (blk * kRowsWaves + wave) * RW;
+    const int nr = r0 >= N ? 0 : (N - r0 < RW ? N - r0 : RW);
+    const int rb = nr ? r0 : 0;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(reinterpret_cast<const unsigned char*>(p.w) + (size_t)rb * rowbytes,
+                                                (uint32_t)nr * rowbytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s + (size_t)rb * G, (uint32_t)nr * G * 2);
+    const __amdgpu_buffer_rsrc_t rbi = make_rsrc(p.b + (size_t)rb * G, (uint32_t)nr * G * 2);
+    // --- 2. the wave's scales and biases (its own LDS region: the wave's reads
+    // of the previous block's have been consumed) and its W rows
+    for (int o = 0; o < sreg; o += 1024) {  // (uniform)
+      copy16(rs, o + lane * 16, sL + o);
+      copy16(rbi, o + lane * 16, bL + o);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    chunk_t wv[RW][J];
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        const uint32_t o = c < C ? (uint32_t)i * rowbytes + (uint32_t)c * CB : kOob;
+        if constexpr (WPC == 4)
+          wv[i][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, kNt));
+        else
+          wv[i][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, kNt));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    wait_vm<RW * J>();  // the scale/bias copies (older than the W loads) have landed
+
+    // --- 3. pass-major: chunk j of four rows of x at a time, then of every row of W
+    PConst kc;
+    kc.init();
+    float part[RW][MR];
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) part[i][m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      const int go = c < C ? (c * 32 / GS) * 2 : 0;
+      const bool full = 64 * (j + 1) <= C;  // (uniform) every lane's chunk exists
+#pragma unroll
+      for (int h = 0; h < MR / MH; ++h) {
+        uint32_t xp[MH][NP];
+        XSums xs[MH];
+#pragma unroll
+        for (int mm = 0; mm < MH; ++mm) {
+          const int m = h * MH + mm;
+#pragma unroll
+          for (int i = 0; i < NP / 4; ++i) {
+            const u32x4 v = full || c < C ? *reinterpret_cast<const u32x4*>(xL + x_slot(m * (K >> 3) + 4 * c + i) * 16)
+                                          : u32x4{0u, 0u, 0u, 0u};
+            xp[mm][4 * i] = v[0];
+            xp[mm][4 * i + 1] = v[1];
+            xp[mm][4 * i + 2] = v[2];
+            xp[mm][4 * i + 3] = v[3];
+          }
+          const f32x4 v =
+              full || c < C ? *reinterpret_cast<const f32x4*>(xsL + (m * C + c) * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+          xs[mm].t[0] = v[0];
+          xs[mm].t[1] = v[1];
+          xs[mm].t[2] = v[2];
+          xs[mm].sx = v[3];
+        }
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+          const float s = bf2f(*reinterpret_cast<const uint16_t*>(sL + i * G * 2 + go));
+          const float b = bf2f(*reinterpret_cast<const uint16_t*>(bL + i * G * 2 + go));
+          const uint32_t* wp = reinterpret_cast<const uint32_t*>(&wv[i][j]);
+          float acc[MH][3];
+#pragma unroll
+          for (int mm = 0; mm < MH; ++mm) acc[mm][0] = acc[mm][1] = acc[mm][2] = 0.f;
+#pragma unroll
+          for (int wd = 0; wd < WPC; ++wd) {
+            uint32_t rq[PPW];
+            punpack<BITS>(wp[wd], kc, rq);
+#pragma unroll
+            for (int mm = 0; mm < MH; ++mm)
+#pragma unroll
+              for (int q = 0; q < PPW; ++q)
+                acc[mm][acc_class<BITS>(q)] = pdot2(rq[q], xp[mm][wd * PPW + q], acc[mm][acc_class<BITS>(q)]);
+          }
+#pragma unroll
+          for (int mm = 0; mm < MH; ++mm)
+            part[i][h * MH + mm] =
+                fmaf(s, dq_finish<BITS>(acc[mm], xs[mm]), fmaf(b, xs[mm].sx, part[i][h * MH + mm]));
+        }
+        // (this step's chains are formed here and the next four rows' LDS reads
+        // stay behind them: otherwise the reads of every pass are hoisted and
+        // the arithmetic sunk, and every pass's pairs are live at once)
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+#pragma unroll
+          for (int mm = 0; mm < MH; ++mm) asm volatile("" : "+v"(part[i][h * MH + mm]));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    float out[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) out[m] = 0.f;
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float tot = wave_sum(part[i][m]);
+        out[m] = lane == i ? tot : out[m];
+      }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y + (size_t)m * N + rb, m < M ? (uint32_t)nr * 2 : 0u);
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(out[m]), ry, lane < RW ? (uint32_t)lane * 2 : kOob, 0, 0);
+    }
+  }  // blocks of rows
+}
+
+// ---------------------------------------------------------------------------
 // Rows per wave: four while a row is at most two 64-lane passes (a wave then
 // has 8-10 KB in flight), two for longer rows.  Measured (M = 1, 4-bit, cold,
 // graph-replayed): 9728 x 2560 RW 4 5.57 us, RW 2 5.63, RW 8 6.49; 2560 x 9728
@@ -362,6 +566,60 @@ static int qmvs_go(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits
 
 int qmvs_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs) {
   return qmvs_go(stream, c, p, bits, gs, false);
+}
+
+// ---------------------------------------------------------------------------
+// Verify rows: RW = 2 (the RW x MR chains share the registers with four rows'
+// pairs); MR = 4 for 3-4 rows, 8 for 5-8; x and its sums must fit the LDS
+// (eight rows at K = 9728 do not: the caller runs two launches of four).
+static constexpr int kRowsRW = 2;
+static int qmvs_rows_mr(int64_t M) { return M <= 4 ? 4 : 8; }
+static int qmvs_rows_lds(int MR, int C, int G) {
+  return qmvs_rows_x_region(MR, C * 32) + (qmvs_rows_xs_bytes(MR, C) + 15) / 16 * 16 +
+         kRowsWaves * 2 * qmvs_sb_region(kRowsRW, G);
+}
+
+bool qmvs_rows_supported(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+  if (M < 1 || M > 8 || (bits != 2 && bits != 4) || gs != 64 || K % 64 != 0 || N < 1) return false;
+  const int64_t C = K / 32;
+  const int J = (int)((C + 63) / 64);
+  if (J > 5) return false;
+  const int64_t rowbytes = C * (bits == 4 ? 16 : 8);
+  if (N * rowbytes >= (int64_t)kOob || N * (K / gs) * 2 >= (int64_t)kOob || K * 2 * M >= (int64_t)kOob ||
+      N * 2 * M >= (int64_t)kOob)
+    return false;
+  return qmvs_rows_lds(qmvs_rows_mr(M), (int)C, (int)(K / gs)) <= 160 * 1024;
+}
+
+template <int BITS, int MR>
+static qmvs_fn qmvs_rows_pick(int J) {
+  switch (J) {
+    case 1: return qmvs_rows_kernel<BITS, 1, kRowsRW, MR>;
+    case 2: return qmvs_rows_kernel<BITS, 2, kRowsRW, MR>;
+    case 3: return qmvs_rows_kernel<BITS, 3, kRowsRW, MR>;
+    case 4: return qmvs_rows_kernel<BITS, 4, kRowsRW, MR>;
+    case 5: return qmvs_rows_kernel<BITS, 5, kRowsRW, MR>;
+    default: return nullptr;
+  }
+}
+
+int qmvs_rows_launch(hipStream_t stream, QmvParams p, int bits) {
+  if (!qmvs_rows_supported(p.M, p.N, p.K, 64, bits) || p.tiles)
+    return set_error(LISAQ_EUNSUPPORTED, "qmvs_rows: M=%d N=%d K=%d bits=%d", p.M, p.N, p.K, bits);
+  const int C = p.K / 32, J = (C + 63) / 64, MR = qmvs_rows_mr(p.M);
+  qmvs_fn fn = bits == 4 ? (MR == 4 ? qmvs_rows_pick<4, 4>(J) : qmvs_rows_pick<4, 8>(J))
+                         : (MR == 4 ? qmvs_rows_pick<2, 4>(J) : qmvs_rows_pick<2, 8>(J));
+  if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmvs_rows: J=%d MR=%d", J, MR);
+  p.chunks = C;
+  p.G = p.K / 64;
+  const int lds = qmvs_rows_lds(MR, C, p.G);
+  if (int rc = allow_dyn_lds((const void*)fn, lds, "qmvs_rows")) return rc;
+  // one workgroup per compute unit (the staged x takes most of the LDS), each
+  // walking blocks of 16 rows of W
+  const int nblk = (p.N + kRowsRW * kRowsWaves - 1) / (kRowsRW * kRowsWaves);
+  const int grid = nblk < 256 ? nblk : 256;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kRowsWaves), lds, stream, p);
+  return check_launch("qmvs_rows");
 }
 
 int qmvs_addnorm_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, int gs) {

@@ -242,16 +242,23 @@ def _one_stream_fits(M, N, K):
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-def test_serial_rows_bitwise_equal_to_single_rows(dev, bits):
-    """array_ops.rs:650-710: batched rows == independent M=1 calls, bitwise."""
-    rng = np.random.default_rng(99 + bits)
-    for N, K in ((64, 512), (2560, 9728), (9728, 2560), (17408, 5120), (1000, 17408)):
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 6, 8])
+def test_serial_rows_bitwise_equal_to_single_rows(dev, force_path, bits, M):
+    """array_ops.rs:650-710 / jit::affine_verify_qmm (matmul.rs:579-664): batched rows == independent
+    M=1 calls, bitwise.  Eight or four rows at a time run on one weight stream (fours where eight rows
+    of x do not fit the LDS: K = 9728), the rest in a pair and/or a single row; long rows (K = 17408) in
+    pairs; the pair path forced for comparison."""
+    rng = np.random.default_rng(99 + bits + 10 * M)
+    for N, K in ((64, 512), (2560, 9728), (9728, 2560), (17408, 5120), (1000, 17408), (77, 2048)):
         w, s, b = np_linear(rng, N, K, bits, 64)
-        x = np_x(rng, 3, K)
+        x = np_x(rng, M, K)
         batched = _run(ops.quantized_matmul_serial_rows, dev, x, w, s, b, 64, bits)
-        for r in range(3):
+        for r in range(M):
             one = _run(ops.quantized_matmul, dev, x[r:r + 1], w, s, b, 64, bits)
-            assert np.array_equal(batched[r:r + 1], one), (N, K, r)
+            assert np.array_equal(batched[r:r + 1], one), (N, K, M, r)
+        force_path("LISAQ_SERIAL_ROWS", "0")
+        assert np.array_equal(_run(ops.quantized_matmul_serial_rows, dev, x, w, s, b, 64, bits), batched), (N, K, M)
+        force_path("LISAQ_SERIAL_ROWS", None)
 
 
 def test_repeated_calls_deterministic(dev):
