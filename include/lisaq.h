@@ -63,7 +63,7 @@ LISAQ_API const char* lisaq_last_error(void);
  * letter 'w','p','d','t','1' (16-row),'3' (32-row); a shape the kernel does
  * not take falls through to the next), LISAQ_QMM_SPLIT (matmul parts over K),
  * LISAQ_GATHER_SHORT, LISAQ_MOE_GU, LISAQ_MOE_FUSED (2 one launch, 1 two
- * launches), LISAQ_MOE_GU_MV (0 = off).
+ * launches), LISAQ_MOE_GU_MV, LISAQ_SERIAL_ROWS (0 = off).
  * LISAQ_PATH_DEFAULT restores the dispatcher's choice.  Process-wide, read by
  * every later dispatch; never read from the environment.  Unknown name:
  * LISAQ_EINVAL_SHAPE. */
@@ -132,9 +132,13 @@ LISAQ_API int lisaq_quantized_matmul_noalloc(void* stream, const void* x, const 
                                    const void* biases, void* y, int64_t M, int64_t N, int64_t K,
                                    int transpose, int group_size, int bits);
 
-/* Replaces ops::quantized_matmul_serial_rows (AO:500-555): each of the M<=8
- * rows gets the same arithmetic as an independent M=1 call (bitwise), and
- * M outside 2..8 falls back to lisaq_quantized_matmul. */
+/* Replaces ops::quantized_matmul_serial_rows (AO:500-555) and serves the
+ * verify rows of jit::affine_verify_qmm (JM:579-664): each of the M<=8 rows
+ * gets the same arithmetic as an independent M=1 call (bitwise), and M
+ * outside 2..8 falls back to lisaq_quantized_matmul.  Eight or four rows
+ * share one pass over W where the one-row kernels serve the shape (group
+ * size 64, K <= 10240); the remaining rows go in pairs.  The path override
+ * LISAQ_SERIAL_ROWS = 0 forces pairs throughout. */
 LISAQ_API int lisaq_quantized_matmul_serial_rows(void* stream, const void* x, const uint32_t* w,
                                        const void* scales, const void* biases, void* y, int64_t M,
                                        int64_t N, int64_t K, int transpose, int group_size,
