@@ -334,9 +334,9 @@ QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   if (P > N) P = (int)N;
   const int T = (int)(((N + P - 1) / P + 15) / 16);
   // x staged in one pass over K, or two where one does not fit (eight rows at
-  // K = 9728)
+  // K = 9728, four at K = 17408)
   int passes = 1, lds = qmvw_lds(MP, K, T, 1);
-  if (lds > 160 * 1024 && K / 512 >= 2 && MP == 8) {
+  if (lds > 160 * 1024 && K / 512 >= 2 && MP >= 4) {
     passes = 2;
     lds = qmvw_lds(MP, K, T, 2);
   }
@@ -375,7 +375,11 @@ static qmvw_fn qmvw_pick_nw(int nw, int ring) {
 
 template <int GS>
 static qmvw_fn qmvw_pick(int mp, int nw, int ring, int passes) {
-  if (passes == 2) return (mp == 8 && nw == 8 && ring == 2) ? qmvw_kernel<8, 8, GS, 2, 2> : nullptr;
+  if (passes == 2 && nw == 8 && ring == 2) {
+    if (mp == 4) return qmvw_kernel<4, 8, GS, 2, 2>;
+    if (mp == 8) return qmvw_kernel<8, 8, GS, 2, 2>;
+  }
+  if (passes == 2) return nullptr;
   if (mp == 1) return qmvw_pick_nw<1, GS>(nw, ring);
   if (mp == 2) return qmvw_pick_nw<2, GS>(nw, ring);
   if (mp == 4) return qmvw_pick_nw<4, GS>(nw, ring);
