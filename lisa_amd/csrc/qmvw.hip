@@ -78,38 +78,45 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
   const int rows = r1 - r0;
   const int T = (rows + 15) >> 4;  // 16-row tiles of the block
   const uint32_t rowbytes = (uint32_t)K / 2;
-  // x staged in p.S_inner passes over K (1, or 2 where all of K does not fit
-  // the LDS): pass ps holds segments [ps * segp, ...); the units of a pass
-  // are padded to a multiple of NW so that every wave reaches the barrier
-  // between passes at the same iteration.  A unit's arithmetic does not
-  // depend on the pass count.
-  constexpr int npass = NP;
-  const int segp = (segs + npass - 1) / npass;        // segments per pass
-  const int U0 = T * (segs < segp ? segs : segp);     // units of pass 0
-  const int U0p = (U0 + NW - 1) / NW * NW;            // (padded)
-  const int U1 = T * segs - U0;                       // units of pass 1 (0 if one pass)
-  const int kswitch = U0p / NW;                       // a wave's first iteration of pass 1
-  const int kiters = kswitch + (U1 + NW - 1) / NW;    // iterations of every wave
-  // unit of iteration k of this wave: tile t, segment g (-1: padding)
+  // x staged in NP passes over K (1, 2 or 4: as few as fit the LDS): pass ps
+  // holds segments [ps * segp, ...); the units of every pass but the last are
+  // padded to a multiple of NW so that every wave reaches the barrier between
+  // passes at the same iteration.  A unit's arithmetic does not depend on the
+  // pass count.
+  static_assert(NP == 1 || NP == 2 || NP == 4, "passes over K");
+  const int segp = (segs + NP - 1) / NP;  // segments per pass
+  int pbase[NP], pspan[NP], pk[NP];        // per pass: first unit, segments, first iteration
+  int kiters = 0;
+  {
+    int base = 0;
+#pragma unroll
+    for (int ps = 0; ps < NP; ++ps) {
+      const int rem = segs - ps * segp;
+      pspan[ps] = rem < 0 ? 0 : (rem < segp ? rem : segp);
+      pbase[ps] = base;
+      pk[ps] = base / NW;
+      const int U = T * pspan[ps];
+      base += ps + 1 < NP ? (U + NW - 1) / NW * NW : U;
+      kiters = (base + NW - 1) / NW;
+    }
+  }
+  // unit of iteration k of this wave: tile t, segment g (false: padding)
   auto unit_of = [&](int k, int& t, int& g) {
     const int u = wave + k * NW;
     if constexpr (NP == 1) {
-      if (u >= U0) return false;
+      if (u >= T * segs) return false;
       t = u / segs;
       g = u - t * segs;
       return true;
     }
-    if (u < U0p) {
-      if (u >= U0) return false;
-      const int sp = segs < segp ? segs : segp;
-      t = u / sp;
-      g = u - t * sp;
-      return true;
-    }
-    const int l = u - U0p, sp = segs - segp;
-    if (l >= U1) return false;
+    int ps = 0;
+#pragma unroll
+    for (int qq = 1; qq < NP; ++qq)
+      if (u >= pbase[qq]) ps = qq;
+    const int l = u - pbase[ps], sp = pspan[ps];
+    if (sp == 0 || l >= T * sp) return false;
     t = l / sp;
-    g = segp + (l - t * sp);
+    g = ps * segp + (l - t * sp);
     return true;
   };
   const int KP = segp * 512;  // columns of x staged per pass
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
   auto compute = [&](int slot, int k) {
     int t = 0, g = 0;
     if (!unit_of(k, t, g)) return;  // (padding of pass 0; wave-uniform)
-    const int gl = g - (g >= segp ? segp : 0);  // segment within the staged pass
+    const int gl = NP == 1 ? g : g % segp;  // segment within the staged pass
     if (a_on) {
 #pragma unroll
       for (int st = 0; st < 4; ++st)
@@ -273,19 +280,22 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
     for (int r = 0; r < RP; ++r) dst[r] = acc[r];
   };
 
-  // two passes: every wave runs the same number of iterations (kiters), so
-  // that the barrier between the passes is reached by all of them at
-  // iteration kswitch; one pass: each wave its own units
+  // several passes: every wave runs the same number of iterations (kiters),
+  // so that the barrier before pass ps is reached by all of them at
+  // iteration pk[ps]; one pass: each wave its own units
+  const int U0 = T * segs;
   const int cnt = NP == 1 ? (wave < U0 ? (U0 - 1 - wave) / NW + 1 : 0) : kiters;
   for (int k0 = 0; k0 < cnt; k0 += RING) {
 #pragma unroll
     for (int d = 0; d < RING; ++d) {
       issue((d + RING - 1) % RING, k0 + d + RING - 1);
       if (k0 + d < cnt) {
-        if (NP > 1 && k0 + d == kswitch) {
-          __syncthreads();  // (every read of pass 0's x done)
-          stage(1);
-        }
+#pragma unroll
+        for (int ps = 1; ps < NP; ++ps)
+          if (k0 + d == pk[ps]) {
+            __syncthreads();  // (every read of the previous pass's x done)
+            stage(ps);
+          }
         compute(d, k0 + d);
       }
     }
@@ -336,9 +346,9 @@ QmvConfig qmvw_config(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   // x staged in one pass over K, or two where one does not fit (eight rows at
   // K = 9728, four at K = 17408)
   int passes = 1, lds = qmvw_lds(MP, K, T, 1);
-  if (lds > 160 * 1024 && K / 512 >= 2 && MP >= 4) {
-    passes = 2;
-    lds = qmvw_lds(MP, K, T, 2);
+  for (int np = 2; np <= 4 && lds > 160 * 1024 && K / 512 >= np && MP >= 4; np *= 2) {
+    passes = np;
+    lds = qmvw_lds(MP, K, T, np);
   }
   if (lds > 160 * 1024) return c;
   c.MR = MP;
@@ -379,7 +389,11 @@ static qmvw_fn qmvw_pick(int mp, int nw, int ring, int passes) {
     if (mp == 4) return qmvw_kernel<4, 8, GS, 2, 2>;
     if (mp == 8) return qmvw_kernel<8, 8, GS, 2, 2>;
   }
-  if (passes == 2) return nullptr;
+  if (passes == 4 && nw == 8 && ring == 2) {
+    if (mp == 4) return qmvw_kernel<4, 8, GS, 2, 4>;
+    if (mp == 8) return qmvw_kernel<8, 8, GS, 2, 4>;
+  }
+  if (passes != 1) return nullptr;
   if (mp == 1) return qmvw_pick_nw<1, GS>(nw, ring);
   if (mp == 2) return qmvw_pick_nw<2, GS>(nw, ring);
   if (mp == 4) return qmvw_pick_nw<4, GS>(nw, ring);
@@ -392,7 +406,7 @@ int qmvw_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
   if (bits == 4 && gs == 64) fn = qmvw_pick<64>(c.MR, c.NW, c.U, c.S_inner);
   else if (bits == 4 && gs == 128) fn = qmvw_pick<128>(c.MR, c.NW, c.U, c.S_inner);
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "qmvw: bits=%d gs=%d rows=%d", bits, gs, c.MR);
-  if (p.tiles || p.M < 1 || p.M > c.MR || p.K % 512 != 0 || grid_x != c.S || (c.S_inner != 1 && c.S_inner != 2) ||
+  if (p.tiles || p.M < 1 || p.M > c.MR || p.K % 512 != 0 || grid_x != c.S || (c.S_inner != 1 && c.S_inner != 2 && c.S_inner != 4) ||
       (int64_t)c.tile_rows * 16 * c.S < p.N || qmvw_lds(c.MR, p.K, c.tile_rows, c.S_inner) != c.lds_bytes)
     return set_error(LISAQ_EINVAL_SHAPE, "qmvw: launch does not match its configuration");
   p.S = c.S;

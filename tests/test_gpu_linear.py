@@ -210,9 +210,9 @@ def test_down_shape_qmv(dev, oracle, bits):
 def test_one_stream_rows_bitwise(dev, oracle, force_path, N, K, gs):
     """The one-stream matvec (1..8 rows of x on one pass over W): every row of an M-row call is bitwise
     equal to the same kernel's one-row call (the matrix-core column of a row never mixes other rows), for
-    every M; every row within tolerance of the oracle.  Eight rows at K = 9728 and four or eight at
-    K = 17408 stage x in two passes over K (all of it does not fit the LDS): bitwise equal to the one-pass
-    one-row call as well."""
+    every M; every row within tolerance of the oracle.  Eight rows at K = 9728 and four at K = 17408
+    stage x in two passes over K, eight at K = 17408 in four (all of it does not fit the LDS): bitwise
+    equal to the one-pass one-row call as well."""
     force_path("LISAQ_QMV_KERNEL", "w")
     rng = np.random.default_rng(N + K + gs)
     w, s, b = np_linear(rng, N, K, 4, gs)
@@ -229,13 +229,13 @@ def test_one_stream_rows_bitwise(dev, oracle, force_path, N, K, gs):
 
 def _one_stream_fits(M, N, K):
     """LDS bytes of the one-stream matvec at its default grid (256 workgroups) within 160 KB, with x
-    staged in one or two passes over K: staged rows of x (each padded by 256 bytes), block sums, per-unit
-    partials (qmvw.hip, qmvw_lds)."""
+    staged in one pass over K, or (four or eight staged rows) two or four: staged rows of x (each padded by
+    256 bytes), block sums, per-unit partials (qmvw.hip, qmvw_lds)."""
     MP = 1 if M == 1 else 2 if M == 2 else 4 if M <= 4 else 8
     RP = min(MP, 4)
     T = (-(-N // 256) + 15) // 16
     segs = K // 512
-    for passes in (1, 2):
+    for passes in ((1, 2, 4) if MP >= 4 else (1,)):
         KP = -(-segs // passes) * 512
         if MP * (2 * KP + 256) + (K // 64) * MP * 4 + T * segs * 64 * RP * 4 <= 160 * 1024:
             return True
