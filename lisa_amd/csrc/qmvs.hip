@@ -296,7 +296,7 @@ __host__ __device__ static inline int qmvs_rows_x_region(int MR, int K) {
   return ((MR * K * 2 + 16 * 64 * kRowsWaves - 1) / (16 * 64 * kRowsWaves)) * (16 * 64 * kRowsWaves);
 }
 
-template <int BITS, int J, int RW, int MR>
+template <int BITS, int J, int RW, int MR, bool PF>
 __global__ __launch_bounds__(64 * kRowsWaves) void qmvs_rows_kernel(QmvParams p) {
   constexpr int GS = 64;
   constexpr int CB = BITS == 4 ? 16 : 8;
@@ -316,8 +316,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void qmvs_rows_kernel(QmvParams p)
   const int sreg = qmvs_sb_region(RW, G);
   unsigned char* xL = lds;                                // x, then its pairs in place (x_slot layout)
   float* xsL = reinterpret_cast<float*>(lds + xreg);      // [MR][C][4] sums
-  unsigned char* sL = lds + xreg + xsreg + wave * 2 * sreg;
-  unsigned char* bL = sL + sreg;
+  unsigned char* sL = lds + xreg + xsreg + wave * (PF ? 4 : 2) * sreg;  // PF: two buffers of [scales][biases]
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2);  // (rows past M read as zero)
 
   // --- 1. the MR rows of x (LDS copies), paired in place once per workgroup
@@ -356,40 +355,81 @@ __global__ __launch_bounds__(64 * kRowsWaves) void qmvs_rows_kernel(QmvParams p)
   }
   lds_sync();
 
-  PConst kc;
-  kc.init();
   const int nblk = (N + RW * kRowsWaves - 1) / (RW * kRowsWaves);
-  for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x) {  // (uniform)
+  // rows of W of block blk for this wave: [rb, rb + nr) (nr = 0 past the end)
+  auto rows_of = [&](int blk, int& nr, int& rb) {
     const int r0 = (blk * kRowsWaves + wave) * RW;
-    const int nr = r0 >= N ? 0 : (N - r0 < RW ? N - r0 : RW);
-    const int rb = nr ? r0 : 0;
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(reinterpret_cast<const unsigned char*>(p.w) + (size_t)rb * rowbytes,
-                                                (uint32_t)nr * rowbytes);
+    nr = r0 >= N ? 0 : (N - r0 < RW ? N - r0 : RW);
+    rb = nr ? r0 : 0;
+  };
+  auto w_rsrc = [&](int nr, int rb) {
+    return make_rsrc(reinterpret_cast<const unsigned char*>(p.w) + (size_t)rb * rowbytes, (uint32_t)nr * rowbytes);
+  };
+  // the wave's scales and biases of block blk into its LDS buffer buf (two
+  // per wave: the next block's are copied while this block is computed)
+  auto copy_sb = [&](int blk, int buf) {
+    int nr, rb;
+    rows_of(blk, nr, rb);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s + (size_t)rb * G, (uint32_t)nr * G * 2);
     const __amdgpu_buffer_rsrc_t rbi = make_rsrc(p.b + (size_t)rb * G, (uint32_t)nr * G * 2);
-    // --- 2. the wave's scales and biases (its own LDS region: the wave's reads
-    // of the previous block's have been consumed) and its W rows
+    unsigned char* s0 = sL + buf * 2 * sreg;
     for (int o = 0; o < sreg; o += 1024) {  // (uniform)
-      copy16(rs, o + lane * 16, sL + o);
-      copy16(rbi, o + lane * 16, bL + o);
+      copy16(rs, o + lane * 16, s0 + o);
+      copy16(rbi, o + lane * 16, s0 + sreg + o);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    chunk_t wv[RW][J];
+  };
+  chunk_t wv[RW][J];
+  auto load_w = [&](__amdgpu_buffer_rsrc_t rw, int i, int j) {
+    const int c = lane + 64 * j;
+    const uint32_t o = c < C ? (uint32_t)i * rowbytes + (uint32_t)c * CB : kOob;
+    if constexpr (WPC == 4)
+      wv[i][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, kNt));
+    else
+      wv[i][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, kNt));
+  };
+  auto load_block = [&](int blk) {  // the W of block blk (every pass)
+    int nr, rb;
+    rows_of(blk, nr, rb);
+    const __amdgpu_buffer_rsrc_t rw = w_rsrc(nr, rb);
 #pragma unroll
     for (int i = 0; i < RW; ++i)
 #pragma unroll
       for (int j = 0; j < J; ++j) {
-        const int c = lane + 64 * j;
-        const uint32_t o = c < C ? (uint32_t)i * rowbytes + (uint32_t)c * CB : kOob;
-        if constexpr (WPC == 4)
-          wv[i][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, kNt));
-        else
-          wv[i][j] = __builtin_bit_cast(chunk_t, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, kNt));
+        load_w(rw, i, j);
         __builtin_amdgcn_sched_barrier(0);
       }
-    wait_vm<RW * J>();  // the scale/bias copies (older than the W loads) have landed
+  };
+  if (PF && (int)blockIdx.x < nblk) {  // (uniform) the first block's copies and W
+    copy_sb(blockIdx.x, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_block(blockIdx.x);
+  }
+  int buf = 0;
+  for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x, buf ^= 1) {  // (uniform)
+    int nr, rb;
+    rows_of(blk, nr, rb);
+    const int nxt = blk + gridDim.x;
+    const bool more = PF && nxt < nblk;  // (uniform) prefetch the next block
+    int nr1 = 0, rb1 = 0;
+    if (more) rows_of(nxt, nr1, rb1);
+    const __amdgpu_buffer_rsrc_t rw1 = w_rsrc(nr1, rb1);
+    if constexpr (!PF) {  // this block's copies and W now (the wave's reads of the last block's are done)
+      copy_sb(blk, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_block(blk);
+    }
+    // this block's copies landed: they are older than its W loads (RW x J),
+    // and loads complete in order; the y stores of the block before are not
+    // loads, so at most RW x J of what is outstanding is younger than them
+    wait_vm<RW * J>();
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) copy_sb(nxt, buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned char* sB = sL + (PF ? buf : 0) * 2 * sreg;
+    const unsigned char* bB = sB + sreg;
 
-    // --- 3. pass-major: chunk j of four rows of x at a time, then of every row of W
+    // --- pass-major: chunk j of four rows of x at a time, then of every row of
+    // W; once pass j is done its W registers take the next block's chunk j
     PConst kc;
     kc.init();
     float part[RW][MR];
@@ -427,8 +467,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void qmvs_rows_kernel(QmvParams p)
         }
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
-          const float s = bf2f(*reinterpret_cast<const uint16_t*>(sL + i * G * 2 + go));
-          const float b = bf2f(*reinterpret_cast<const uint16_t*>(bL + i * G * 2 + go));
+          const float s = bf2f(*reinterpret_cast<const uint16_t*>(sB + i * G * 2 + go));
+          const float b = bf2f(*reinterpret_cast<const uint16_t*>(bB + i * G * 2 + go));
           const uint32_t* wp = reinterpret_cast<const uint32_t*>(&wv[i][j]);
           float acc[MH][3];
 #pragma unroll
@@ -457,6 +497,13 @@ __global__ __launch_bounds__(64 * kRowsWaves) void qmvs_rows_kernel(QmvParams p)
           for (int mm = 0; mm < MH; ++mm) asm volatile("" : "+v"(part[i][h * MH + mm]));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+      }
+      if (more) {  // (uniform) pass j's W registers take the next block's chunk j
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+          load_w(rw1, i, j);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
     float out[MR];
@@ -574,9 +621,16 @@ int qmvs_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
 // (eight rows at K = 9728 do not: the caller runs two launches of four).
 static constexpr int kRowsRW = 2;
 static int qmvs_rows_mr(int64_t M) { return M <= 4 ? 4 : 8; }
+// the next block's W and scales/biases loaded during this block's arithmetic
+// (two scale/bias buffers per wave) except with eight rows of x from three
+// passes on, where the registers then spill (north star, 8 rows: 61.4 us
+// with, 51.7 without; 4 rows 25.0 with, 27.1 without), and at five passes
+// (248 registers: 2560 x 9728, 4 rows 12.4 with, 12.2 without)
+static bool qmvs_rows_pf(int MR, int J) { return J <= 2 || (MR == 4 && J <= 4); }
 static int qmvs_rows_lds(int MR, int C, int G) {
+  const int J = (C + 63) / 64;
   return qmvs_rows_x_region(MR, C * 32) + (qmvs_rows_xs_bytes(MR, C) + 15) / 16 * 16 +
-         kRowsWaves * 2 * qmvs_sb_region(kRowsRW, G);
+         kRowsWaves * (qmvs_rows_pf(MR, J) ? 4 : 2) * qmvs_sb_region(kRowsRW, G);
 }
 
 bool qmvs_rows_supported(int64_t M, int64_t N, int64_t K, int gs, int bits) {
@@ -591,14 +645,15 @@ bool qmvs_rows_supported(int64_t M, int64_t N, int64_t K, int gs, int bits) {
   return qmvs_rows_lds(qmvs_rows_mr(M), (int)C, (int)(K / gs)) <= 160 * 1024;
 }
 
+// (PF as qmvs_rows_pf)
 template <int BITS, int MR>
 static qmvs_fn qmvs_rows_pick(int J) {
   switch (J) {
-    case 1: return qmvs_rows_kernel<BITS, 1, kRowsRW, MR>;
-    case 2: return qmvs_rows_kernel<BITS, 2, kRowsRW, MR>;
-    case 3: return qmvs_rows_kernel<BITS, 3, kRowsRW, MR>;
-    case 4: return qmvs_rows_kernel<BITS, 4, kRowsRW, MR>;
-    case 5: return qmvs_rows_kernel<BITS, 5, kRowsRW, MR>;
+    case 1: return qmvs_rows_kernel<BITS, 1, kRowsRW, MR, true>;
+    case 2: return qmvs_rows_kernel<BITS, 2, kRowsRW, MR, true>;
+    case 3: return qmvs_rows_kernel<BITS, 3, kRowsRW, MR, MR == 4>;
+    case 4: return qmvs_rows_kernel<BITS, 4, kRowsRW, MR, MR == 4>;
+    case 5: return qmvs_rows_kernel<BITS, 5, kRowsRW, MR, false>;
     default: return nullptr;
   }
 }
