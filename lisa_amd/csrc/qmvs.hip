@@ -303,8 +303,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void qmvs_rows_kernel(QmvParams p)
   constexpr int WPC = CB / 4;
   constexpr int PPW = 16 / BITS;
   constexpr int NP = WPC * PPW;
-  constexpr int MH = 4;  // rows of x per step inside a pass
-  static_assert(MR % MH == 0, "rows of x in fours");
+  constexpr int MH = (MR == 8 && J >= 3) ? 2 : 4;  // rows of x per step inside a pass
+  static_assert(MR % MH == 0, "rows of x in steps of MH");
   typedef uint32_t chunk_t __attribute__((ext_vector_type(WPC)));
 
   const int t = threadIdx.x, lane = t & 63;
@@ -622,11 +622,12 @@ int qmvs_launch(hipStream_t stream, const QmvConfig& c, QmvParams p, int bits, i
 static constexpr int kRowsRW = 2;
 static int qmvs_rows_mr(int64_t M) { return M <= 4 ? 4 : 8; }
 // the next block's W and scales/biases loaded during this block's arithmetic
-// (two scale/bias buffers per wave) except with eight rows of x from three
-// passes on, where the registers then spill (north star, 8 rows: 61.4 us
-// with, 51.7 without; 4 rows 25.0 with, 27.1 without), and at five passes
-// (248 registers: 2560 x 9728, 4 rows 12.4 with, 12.2 without)
-static bool qmvs_rows_pf(int MR, int J) { return J <= 2 || (MR == 4 && J <= 4); }
+// (two scale/bias buffers per wave) up to three passes (four with four rows
+// of x), eight rows of x from three passes on then held two at a time
+// (north star, 8 rows: 44.8 us, 51.7 without the prefetch, 61.4 with it and
+// four x rows at a time: spills; 4 rows 25.0 with, 27.1 without); not at five
+// passes (248 registers: 2560 x 9728, 4 rows 12.4 with, 12.2 without)
+static bool qmvs_rows_pf(int MR, int J) { return J <= 3 || (MR == 4 && J <= 4); }
 static int qmvs_rows_lds(int MR, int C, int G) {
   const int J = (C + 63) / 64;
   return qmvs_rows_x_region(MR, C * 32) + (qmvs_rows_xs_bytes(MR, C) + 15) / 16 * 16 +
@@ -651,7 +652,7 @@ static qmvs_fn qmvs_rows_pick(int J) {
   switch (J) {
     case 1: return qmvs_rows_kernel<BITS, 1, kRowsRW, MR, true>;
     case 2: return qmvs_rows_kernel<BITS, 2, kRowsRW, MR, true>;
-    case 3: return qmvs_rows_kernel<BITS, 3, kRowsRW, MR, MR == 4>;
+    case 3: return qmvs_rows_kernel<BITS, 3, kRowsRW, MR, true>;
     case 4: return qmvs_rows_kernel<BITS, 4, kRowsRW, MR, MR == 4>;
     case 5: return qmvs_rows_kernel<BITS, 5, kRowsRW, MR, false>;
     default: return nullptr;
