@@ -205,7 +205,7 @@ def test_down_shape_qmv(dev, oracle, bits):
         assert_close_bf16(got, ref, what=f"down-shape qmv M={M} bits={bits}")
 
 
-@pytest.mark.parametrize("N,K,gs", [(17408, 5120, 64), (9728, 2560, 64), (2560, 9728, 64), (5120, 17408, 64), (1000, 1024, 64),
+@pytest.mark.parametrize("N,K,gs", [(17408, 5120, 64), (9728, 2560, 64), (2560, 9728, 64), (5120, 17408, 64), (5120, 17408, 128), (1000, 1024, 64),
                                     (777, 2048, 128), (5, 512, 64)])
 def test_one_stream_rows_bitwise(dev, oracle, force_path, N, K, gs):
     """The one-stream matvec (1..8 rows of x on one pass over W): every row of an M-row call is bitwise
