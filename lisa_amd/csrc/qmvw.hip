@@ -33,9 +33,10 @@
 // straight from memory would be 16 rows x 64 bytes per load, which streams
 // slower), the B operand of each step is then taken lane-wise (step 2p) or
 // with a rotate by 8 lanes (step 2p+1).  Per-unit partials go to LDS and are
-// summed after one barrier.  x is staged once per workgroup in LDS in the
-// unpack order of the codes (x0,x4,x1,x5,x2,x6,x3,x7 per 8 codes), with the
-// per-block sums of x beside it.  All global memory operations are buffer
+// summed after one barrier.  x is staged per workgroup in LDS in the unpack
+// order of the codes (x0,x4,x1,x5,x2,x6,x3,x7 per 8 codes), with the
+// per-block sums of x beside it: all of K at once, or in two or four passes
+// over K where that does not fit (four or eight rows of x at long K).  All global memory operations are buffer
 // operations with exact ranges: rows past the block read as zero and stores
 // past the output are dropped.
 #include "lisaq_common.h"
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(64 * NW) void qmvw_kernel(QmvParams p) {
 
   auto compute = [&](int slot, int k) {
     int t = 0, g = 0;
-    if (!unit_of(k, t, g)) return;  // (padding of pass 0; wave-uniform)
+    if (!unit_of(k, t, g)) return;  // (padding of a pass; wave-uniform)
     const int gl = NP == 1 ? g : g % segp;  // segment within the staged pass
     if (a_on) {
 #pragma unroll
