@@ -284,9 +284,10 @@ __global__ __launch_bounds__(256) void qmvs_kernel(QmvParams p) {
 // copied into LDS as in the kernel above, the workgroup pairs it in place
 // (the pairs of a chunk are a permutation of its 16 words) with the chunks'
 // sums beside, and for pass j each wave reads the pairs of its lanes' chunk j,
-// four rows of x at a time, then runs that chunk of all its RW rows of W,
-// carrying RW x MR partial chains in registers; each chain's order is
-// unchanged.
+// four rows of x at a time (two for eight rows from three passes on), then
+// runs that chunk of all its RW rows of W, carrying RW x MR partial chains in
+// registers; each chain's order is unchanged.  PF: while a block of rows is
+// computed, the next block's W and scales/biases are loaded.
 __host__ __device__ static inline int qmvs_rows_xs_bytes(int MR, int C) { return MR * C * 16; }
 // eight waves per workgroup: the staged rows of x (80 KB for eight rows at
 // K = 5120) are shared by twice the rows of W, and a compute unit still holds
