@@ -12,10 +12,10 @@
 //    :585-703): every weight dequantized to T, w = T(scale * q + bias) from an
 //    f32 fma, then y = x . w^T with f32 accumulation, rounded to T once.
 //
-// These are straightforward kernels (one wave per output row for the
-// matvec, 64 x 64 register-tiled f32 FMA for the matmul): correct for every
-// dtype and width, not tuned -- the bf16 2/4-bit shapes the engine runs take
-// the MFMA kernels instead.
+// Kernels: one wave per output row for the matvec; for the matmul the matrix
+// cores with bf16/f16 (below), else 64 x 64 register-tiled f32 FMA -- correct
+// for every dtype and width, not tuned further; the bf16 2/4-bit shapes the
+// engine runs take the tuned kernels instead.
 #include "lisaq_common.h"
 #include "qmv.h"
 
@@ -161,7 +161,137 @@ __global__ __launch_bounds__(256) void qmm_typed_kernel(const void* x, const uin
     }
 }
 
+// Matmul on the matrix cores for the 16-bit compute dtypes (bf16, f16): the
+// same contract -- every weight T(fma(scale, q, bias)), f32 accumulation, one
+// rounding -- with v_mfma_f32_16x16x32_{bf16,f16}.  64 x 64 output tile per
+// workgroup of four waves (each 32 x 32: 2 x 2 matrix tiles), K in steps of
+// 32: each thread stages 8 values of x and dequantizes 8 weights of one row
+// into two LDS buffers (rows padded to 80 bytes: a quarter-wave's 16-byte
+// fragment reads hit distinct banks), so one barrier per step; the next
+// step's x and code words are loaded while the current step's matrix
+// instructions run.  x must be 16-byte aligned (the host checks).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <int DT>
+__device__ __forceinline__ uint16_t bits16(float v) {
+  if constexpr (DT == 0) return f2bf(v);
+  else return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+template <int DT, int BITS, int GS>
+__global__ __launch_bounds__(256) void qmm_typed_mfma_kernel(const void* x, const uint32_t* w, const void* s,
+                                                             const void* b, void* y, int M, int N, int K) {
+  static_assert(DT == 0 || DT == 2, "16-bit compute dtypes");
+  constexpr int BM = 64, BN = 64, BK = 32, RS = 40;  // LDS row stride: 40 16-bit values (80 bytes)
+  __shared__ __attribute__((aligned(16))) uint16_t xa[2][BM * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t wb[2][BN * RS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;  // the wave's 32 x 32 quarter
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int G = K / GS;
+  // staging role: row sr of the tile, values 8 c8 .. 8 c8 + 7 of the step
+  const int sr = tid >> 2, c8 = (tid & 3) * 8;
+  const bool xok = m0 + sr < M;
+  const int nr = n0 + sr < N ? n0 + sr : N - 1;  // (rows past N: never stored)
+  const uint16_t* xrow = static_cast<const uint16_t*>(x) + (int64_t)(xok ? m0 + sr : 0) * K;
+  const uint32_t* wrow = w + (int64_t)nr * (K / (32 / BITS));
+  u32x4 xv;
+  uint32_t cw[BITS == 8 ? 2 : 1];
+  float sc, bi;
+  auto fetch = [&](int k0) {
+    const int k = k0 + c8;
+    xv = xok ? *reinterpret_cast<const u32x4*>(xrow + k) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (BITS == 8) {
+      cw[0] = wrow[k / 4];
+      cw[1] = wrow[k / 4 + 1];
+    } else if constexpr (BITS == 4) {
+      cw[0] = wrow[k / 8];
+    } else {
+      cw[0] = wrow[k / 16] >> (2 * (k % 16));
+    }
+    const int g = k / GS;  // (8 consecutive codes lie in one group: GS >= 32)
+    sc = ld<DT>(s, (int64_t)nr * G + g);
+    bi = ld<DT>(b, (int64_t)nr * G + g);
+  };
+  auto stage = [&](int buf) {
+    *reinterpret_cast<u32x4*>(&xa[buf][sr * RS + c8]) = xv;
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      uint32_t q0, q1;
+      if constexpr (BITS == 8) {
+        q0 = (cw[j / 4] >> (8 * (j % 4))) & 0xFFu;
+        q1 = (cw[j / 4] >> (8 * (j % 4 + 1))) & 0xFFu;
+      } else {
+        q0 = (cw[0] >> (BITS * j)) & ((1u << BITS) - 1u);
+        q1 = (cw[0] >> (BITS * (j + 1))) & ((1u << BITS) - 1u);
+      }
+      h[j / 2] = (uint32_t)bits16<DT>(fmaf(sc, (float)q0, bi)) |
+                 ((uint32_t)bits16<DT>(fmaf(sc, (float)q1, bi)) << 16);
+    }
+    *reinterpret_cast<u32x4*>(&wb[buf][sr * RS + c8]) = u32x4{h[0], h[1], h[2], h[3]};
+  };
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // fragment reads: row (lane & 15) of a 16-row tile, k values 8 (lane >> 4) ..
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int k0 = 0, buf = 0; k0 < K; k0 += BK, buf ^= 1) {
+    const bool more = k0 + BK < K;
+    if (more) fetch(k0 + BK);
+    u32x4 af[2], bf[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      af[i] = *reinterpret_cast<const u32x4*>(&xa[buf][(wm + 16 * i + fr) * RS + fk]);
+      bf[i] = *reinterpret_cast<const u32x4*>(&wb[buf][(wn + 16 * i + fr) * RS + fk]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if constexpr (DT == 0)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af[i]), as_bf16x8(bf[j]), acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af[i]),
+                                                             __builtin_bit_cast(f16x8, bf[j]), acc[i][j], 0, 0, 0);
+      }
+    if (more) stage(buf ^ 1);  // (buffer buf ^ 1 was last read before the previous barrier)
+    __syncthreads();
+  }
+  // output element (row 4 (lane >> 4) + e, column lane & 15) of each 16 x 16 tile
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + wm + 16 * i + 4 * (lane >> 4) + e, n = n0 + wn + 16 * j + (lane & 15);
+        if (m < M && n < N) st<DT>(y, (int64_t)m * N + n, acc[i][j][e]);
+      }
+}
+
 typedef void (*typed_fn)(const void*, const uint32_t*, const void*, const void*, void*, int, int, int);
+
+template <int DT, int BITS>
+typed_fn pick_mfma_gs(int gs) {
+  if (gs == 32) return qmm_typed_mfma_kernel<DT, BITS, 32>;
+  if (gs == 64) return qmm_typed_mfma_kernel<DT, BITS, 64>;
+  if (gs == 128) return qmm_typed_mfma_kernel<DT, BITS, 128>;
+  return nullptr;
+}
+
+template <int DT>
+typed_fn pick_mfma(int bits, int gs) {
+  if (bits == 2) return pick_mfma_gs<DT, 2>(gs);
+  if (bits == 4) return pick_mfma_gs<DT, 4>(gs);
+  if (bits == 8) return pick_mfma_gs<DT, 8>(gs);
+  return nullptr;
+}
 
 template <bool MV, int DT, int BITS>
 typed_fn pick_gs(int gs) {
@@ -191,7 +321,12 @@ typed_fn pick(int dtype, int bits, int gs) {
 
 int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* w, const void* s, const void* b,
                     void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype) {
-  const typed_fn fn = matvec ? pick<true>(dtype, bits, gs) : pick<false>(dtype, bits, gs);
+  typed_fn fn = matvec ? pick<true>(dtype, bits, gs) : pick<false>(dtype, bits, gs);
+  // 16-bit compute dtypes: the matrix-core matmul (x 16-byte aligned)
+  if (!matvec && fn && reinterpret_cast<uintptr_t>(x) % 16 == 0 && tune_int("LISAQ_TYPED_MFMA", 1) != 0) {
+    if (dtype == LISAQ_DTYPE_BF16) fn = pick_mfma<0>(bits, gs);
+    else if (dtype == LISAQ_DTYPE_F16) fn = pick_mfma<2>(bits, gs);
+  }
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "quantized_matmul_typed: dtype=%d bits=%d gs=%d", dtype, bits, gs);
   // grid.y carries the 64-row tiles of M (at most 65535 of them)
   if (!matvec && (M + 63) / 64 > 65535)

@@ -34,7 +34,7 @@ def _close(got, ref, dtype, what):
 @pytest.mark.parametrize("dtype,bits", [("f16", 2), ("f16", 4), ("f16", 8), ("f32", 2), ("f32", 4), ("f32", 8),
                                         ("bf16", 8)])
 @pytest.mark.parametrize("gs", [32, 64, 128])
-@pytest.mark.parametrize("M", [1, 5, 40])
+@pytest.mark.parametrize("M", [1, 5, 40, 130])
 def test_quantized_matmul_typed(dev, oracle, dtype, bits, gs, M):
     import torch
 
