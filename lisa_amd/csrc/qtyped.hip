@@ -102,6 +102,104 @@ __global__ __launch_bounds__(256) void qmv_typed_kernel(const void* x, const uin
   }
 }
 
+// The same matvec with x staged in LDS: up to four rows of x (in T) copied
+// once per workgroup, the workgroup's waves then walk rows of W with a grid
+// stride, each lane loading its chunk's code words at once; the fused
+// multiply-adds are those of the kernel above in the same order (the same
+// bits).  LDS: MB x K values of T.
+template <int DT>
+__device__ __forceinline__ void ld8(const unsigned char* xl, int i, float* v) {  // values i .. i+7 of the LDS row image
+  if constexpr (DT == 1) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(xl + i * 4), c = *reinterpret_cast<const f32x4*>(xl + i * 4 + 16);
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3]; v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
+  } else {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(xl + i * 2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (DT == 0) {
+        v[2 * e] = __uint_as_float(a[e] << 16);
+        v[2 * e + 1] = __uint_as_float(a[e] & 0xffff0000u);
+      } else {
+        v[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(a[e] & 0xffffu));
+        v[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(a[e] >> 16));
+      }
+    }
+  }
+}
+
+template <int DT, int BITS, int GS>
+__global__ __launch_bounds__(256) void qmv_typed_lds_kernel(const void* x, const uint32_t* w, const void* s,
+                                                            const void* b, void* y, int M, int N, int K, int MB) {
+  constexpr int MBX = 4;     // rows of x per group (at most)
+  constexpr int WPC = BITS;  // u32 words per 32-code chunk
+  constexpr int SZ = DT == 1 ? 4 : 2;
+  extern __shared__ __attribute__((aligned(16))) unsigned char xsm[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int C = K / 32, G = K / GS;
+  const int64_t wstride = K / (32 / BITS);
+  for (int m0 = 0; m0 < M; m0 += MB) {
+    const int mb = M - m0 < MB ? M - m0 : MB;
+    __syncthreads();  // (the previous group's reads are done)
+    {
+      const unsigned char* src = static_cast<const unsigned char*>(x) + (int64_t)m0 * K * SZ;
+      const int nbytes = mb * K * SZ;  // (K * SZ: a multiple of 64)
+      for (int i = tid * 16; i < nbytes; i += 256 * 16)
+        *reinterpret_cast<u32x4*>(xsm + i) = *reinterpret_cast<const u32x4*>(src + i);
+    }
+    __syncthreads();
+    for (int n = blockIdx.x * 4 + wave; n < N; n += gridDim.x * 4) {  // (wave-uniform)
+      const uint32_t* wrow = w + (int64_t)n * wstride;
+      float part[MBX];
+#pragma unroll
+      for (int r = 0; r < MBX; ++r) part[r] = 0.f;
+      for (int c = lane; c < C; c += 64) {
+        uint32_t wv[WPC];
+        if constexpr (WPC == 2) {
+          const uint2 v = *reinterpret_cast<const uint2*>(wrow + c * 2);
+          wv[0] = v.x;
+          wv[1] = v.y;
+        } else {
+#pragma unroll
+          for (int i = 0; i < WPC; i += 4) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(wrow + c * WPC + i);
+            wv[i] = v[0];
+            wv[i + 1] = v[1];
+            wv[i + 2] = v[2];
+            wv[i + 3] = v[3];
+          }
+        }
+        const int g = c * 32 / GS;
+        const float sc = ld<DT>(s, (int64_t)n * G + g), bi = ld<DT>(b, (int64_t)n * G + g);
+#pragma unroll
+        for (int r = 0; r < MBX; ++r) {
+          if (r >= mb) break;
+          const unsigned char* xr = xsm + (int64_t)r * K * SZ;
+          float dot = 0.f, xs = 0.f;
+#pragma unroll
+          for (int j8 = 0; j8 < 32; j8 += 8) {
+            float xv[8];
+            ld8<DT>(xr, c * 32 + j8, xv);
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+              const int j = j8 + jj;
+              const float q = (float)((wv[j / (32 / BITS)] >> (BITS * (j % (32 / BITS)))) & ((1u << BITS) - 1u));
+              dot = fmaf(xv[jj], q, dot);
+              xs += xv[jj];
+            }
+          }
+          part[r] = fmaf(sc, dot, fmaf(bi, xs, part[r]));
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < MBX; ++r) {
+        if (r >= mb) break;
+        const float t = wsum64(part[r]);
+        if (lane == 0) st<DT>(y, (int64_t)(m0 + r) * N + n, t);
+      }
+    }
+  }
+}
+
 // Matmul: 64 x 64 output tile per workgroup, K in steps of 32 through LDS (x
 // and the dequantized, T-rounded weights, both as f32), 4 x 4 outputs per
 // thread.
@@ -277,6 +375,31 @@ __global__ __launch_bounds__(256) void qmm_typed_mfma_kernel(const void* x, cons
 
 typedef void (*typed_fn)(const void*, const uint32_t*, const void*, const void*, void*, int, int, int);
 
+typedef void (*typed_mv_fn)(const void*, const uint32_t*, const void*, const void*, void*, int, int, int, int);
+
+template <int DT, int BITS>
+typed_mv_fn pick_mv_lds_gs(int gs) {
+  if (gs == 32) return qmv_typed_lds_kernel<DT, BITS, 32>;
+  if (gs == 64) return qmv_typed_lds_kernel<DT, BITS, 64>;
+  if (gs == 128) return qmv_typed_lds_kernel<DT, BITS, 128>;
+  return nullptr;
+}
+
+template <int DT>
+typed_mv_fn pick_mv_lds_bits(int bits, int gs) {
+  if (bits == 2) return pick_mv_lds_gs<DT, 2>(gs);
+  if (bits == 4) return pick_mv_lds_gs<DT, 4>(gs);
+  if (bits == 8) return pick_mv_lds_gs<DT, 8>(gs);
+  return nullptr;
+}
+
+typed_mv_fn pick_mv_lds(int dtype, int bits, int gs) {
+  if (dtype == LISAQ_DTYPE_BF16) return pick_mv_lds_bits<0>(bits, gs);
+  if (dtype == LISAQ_DTYPE_F32) return pick_mv_lds_bits<1>(bits, gs);
+  if (dtype == LISAQ_DTYPE_F16) return pick_mv_lds_bits<2>(bits, gs);
+  return nullptr;
+}
+
 template <int DT, int BITS>
 typed_fn pick_mfma_gs(int gs) {
   if (gs == 32) return qmm_typed_mfma_kernel<DT, BITS, 32>;
@@ -331,6 +454,27 @@ int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* 
   // grid.y carries the 64-row tiles of M (at most 65535 of them)
   if (!matvec && (M + 63) / 64 > 65535)
     return set_error(LISAQ_EINVAL_SHAPE, "quantized_matmul_typed: M=%lld exceeds %d rows", (long long)M, 65535 * 64);
+  // matvec with x staged in LDS (rows of x per group as the LDS allows, at
+  // most four; x 16-byte aligned): for f32, and for 16-bit x from four rows
+  // on.  Measured (gs 64, graph-replayed; global-x kernel -> this one):
+  // 17408 x 5120 4-bit f32 M=1 51.8 -> 27.5 us, M=4 161.9 -> 96.0, f16 M=4
+  // 62.2 -> 52.2 but f16 M=1 19.7 -> 24.8 (one row: the global-x kernel's
+  // 4352 small workgroups hide the x reads better than 1024 staging ones)
+  const int xsz = dtype == LISAQ_DTYPE_F32 ? 4 : 2;
+  const int64_t mbl = (160 * 1024) / (K * xsz);
+  if (matvec && mbl >= 1 && (dtype == LISAQ_DTYPE_F32 || M >= 4) && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(w) % 16 == 0 && tune_int("LISAQ_TYPED_MV_LDS", 1) != 0) {
+    typed_mv_fn fl = pick_mv_lds(dtype, bits, gs);
+    if (fl) {
+      const int MB = (int)(mbl < 4 ? mbl : 4) < M ? (int)(mbl < 4 ? mbl : 4) : (int)M;
+      const int lds = (int)(MB * K * xsz);
+      if (int rc = allow_dyn_lds((const void*)fl, lds, "quantized_matmul_typed")) return rc;
+      const int64_t rows4 = (N + 3) / 4;
+      const unsigned grid = (unsigned)(rows4 < 1024 ? rows4 : 1024);
+      hipLaunchKernelGGL(fl, dim3(grid), dim3(256), lds, st, x, w, s, b, y, (int)M, (int)N, (int)K, MB);
+      return check_launch("quantized_matmul_typed");
+    }
+  }
   if (matvec)
     hipLaunchKernelGGL(fn, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, w, s, b, y, (int)M, (int)N, (int)K);
   else
