@@ -276,64 +276,82 @@ __device__ __forceinline__ uint16_t bits16(float v) {
   else return __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
-template <int DT, int BITS, int GS>
+template <int DT, int BITS, int GS, int TB>
 __global__ __launch_bounds__(256) void qmm_typed_mfma_kernel(const void* x, const uint32_t* w, const void* s,
                                                              const void* b, void* y, int M, int N, int K) {
   static_assert(DT == 0 || DT == 2, "16-bit compute dtypes");
-  constexpr int BM = 64, BN = 64, BK = 32, RS = 40;  // LDS row stride: 40 16-bit values (80 bytes)
+  static_assert(TB == 1 || TB == 2, "tile scale");
+  // TB: 64 TB x 64 TB output tile, each wave 32 TB x 32 TB (2 TB x 2 TB matrix tiles)
+  constexpr int BM = 64 * TB, BN = 64 * TB, BK = 32, RS = 40;  // LDS row stride: 40 16-bit values (80 bytes)
+  constexpr int FT = 2 * TB;                                   // matrix tiles per wave and side
   __shared__ __attribute__((aligned(16))) uint16_t xa[2][BM * RS];
   __shared__ __attribute__((aligned(16))) uint16_t wb[2][BN * RS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;  // the wave's 32 x 32 quarter
+  const int wm = (wave >> 1) * 32 * TB, wn = (wave & 1) * 32 * TB;  // the wave's quarter
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int G = K / GS;
-  // staging role: row sr of the tile, values 8 c8 .. 8 c8 + 7 of the step
+  // staging role: rows sr + 64 t of the tile (t < TB), values 8 c8 .. 8 c8 + 7 of the step
   const int sr = tid >> 2, c8 = (tid & 3) * 8;
-  const bool xok = m0 + sr < M;
-  const int nr = n0 + sr < N ? n0 + sr : N - 1;  // (rows past N: never stored)
-  const uint16_t* xrow = static_cast<const uint16_t*>(x) + (int64_t)(xok ? m0 + sr : 0) * K;
-  const uint32_t* wrow = w + (int64_t)nr * (K / (32 / BITS));
-  u32x4 xv;
-  uint32_t cw[BITS == 8 ? 2 : 1];
-  float sc, bi;
+  bool xok[TB];
+  int nr[TB];
+  const uint16_t* xrow[TB];
+  const uint32_t* wrow[TB];
+#pragma unroll
+  for (int t = 0; t < TB; ++t) {
+    const int r = sr + 64 * t;
+    xok[t] = m0 + r < M;
+    nr[t] = n0 + r < N ? n0 + r : N - 1;  // (rows past N: never stored)
+    xrow[t] = static_cast<const uint16_t*>(x) + (int64_t)(xok[t] ? m0 + r : 0) * K;
+    wrow[t] = w + (int64_t)nr[t] * (K / (32 / BITS));
+  }
+  u32x4 xv[TB];
+  uint32_t cw[TB][BITS == 8 ? 2 : 1];
+  float sc[TB], bi[TB];
   auto fetch = [&](int k0) {
     const int k = k0 + c8;
-    xv = xok ? *reinterpret_cast<const u32x4*>(xrow + k) : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (BITS == 8) {
-      cw[0] = wrow[k / 4];
-      cw[1] = wrow[k / 4 + 1];
-    } else if constexpr (BITS == 4) {
-      cw[0] = wrow[k / 8];
-    } else {
-      cw[0] = wrow[k / 16] >> (2 * (k % 16));
-    }
     const int g = k / GS;  // (8 consecutive codes lie in one group: GS >= 32)
-    sc = ld<DT>(s, (int64_t)nr * G + g);
-    bi = ld<DT>(b, (int64_t)nr * G + g);
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      xv[t] = xok[t] ? *reinterpret_cast<const u32x4*>(xrow[t] + k) : u32x4{0u, 0u, 0u, 0u};
+      if constexpr (BITS == 8) {
+        cw[t][0] = wrow[t][k / 4];
+        cw[t][1] = wrow[t][k / 4 + 1];
+      } else if constexpr (BITS == 4) {
+        cw[t][0] = wrow[t][k / 8];
+      } else {
+        cw[t][0] = wrow[t][k / 16] >> (2 * (k % 16));
+      }
+      sc[t] = ld<DT>(s, (int64_t)nr[t] * G + g);
+      bi[t] = ld<DT>(b, (int64_t)nr[t] * G + g);
+    }
   };
   auto stage = [&](int buf) {
-    *reinterpret_cast<u32x4*>(&xa[buf][sr * RS + c8]) = xv;
-    uint32_t h[4];
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      uint32_t q0, q1;
-      if constexpr (BITS == 8) {
-        q0 = (cw[j / 4] >> (8 * (j % 4))) & 0xFFu;
-        q1 = (cw[j / 4] >> (8 * (j % 4 + 1))) & 0xFFu;
-      } else {
-        q0 = (cw[0] >> (BITS * j)) & ((1u << BITS) - 1u);
-        q1 = (cw[0] >> (BITS * (j + 1))) & ((1u << BITS) - 1u);
+    for (int t = 0; t < TB; ++t) {
+      const int r = sr + 64 * t;
+      *reinterpret_cast<u32x4*>(&xa[buf][r * RS + c8]) = xv[t];
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        uint32_t q0, q1;
+        if constexpr (BITS == 8) {
+          q0 = (cw[t][j / 4] >> (8 * (j % 4))) & 0xFFu;
+          q1 = (cw[t][j / 4] >> (8 * (j % 4 + 1))) & 0xFFu;
+        } else {
+          q0 = (cw[t][0] >> (BITS * j)) & ((1u << BITS) - 1u);
+          q1 = (cw[t][0] >> (BITS * (j + 1))) & ((1u << BITS) - 1u);
+        }
+        h[j / 2] = (uint32_t)bits16<DT>(fmaf(sc[t], (float)q0, bi[t])) |
+                   ((uint32_t)bits16<DT>(fmaf(sc[t], (float)q1, bi[t])) << 16);
       }
-      h[j / 2] = (uint32_t)bits16<DT>(fmaf(sc, (float)q0, bi)) |
-                 ((uint32_t)bits16<DT>(fmaf(sc, (float)q1, bi)) << 16);
+      *reinterpret_cast<u32x4*>(&wb[buf][r * RS + c8]) = u32x4{h[0], h[1], h[2], h[3]};
     }
-    *reinterpret_cast<u32x4*>(&wb[buf][sr * RS + c8]) = u32x4{h[0], h[1], h[2], h[3]};
   };
-  f32x4 acc[2][2];
+  f32x4 acc[FT][FT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   // fragment reads: row (lane & 15) of a 16-row tile, k values 8 (lane >> 4) ..
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   fetch(0);
@@ -342,16 +360,16 @@ __global__ __launch_bounds__(256) void qmm_typed_mfma_kernel(const void* x, cons
   for (int k0 = 0, buf = 0; k0 < K; k0 += BK, buf ^= 1) {
     const bool more = k0 + BK < K;
     if (more) fetch(k0 + BK);
-    u32x4 af[2], bf[2];
+    u32x4 af[FT], bf[FT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < FT; ++i) {
       af[i] = *reinterpret_cast<const u32x4*>(&xa[buf][(wm + 16 * i + fr) * RS + fk]);
       bf[i] = *reinterpret_cast<const u32x4*>(&wb[buf][(wn + 16 * i + fr) * RS + fk]);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < FT; ++j) {
         if constexpr (DT == 0)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af[i]), as_bf16x8(bf[j]), acc[i][j], 0, 0, 0);
         else
@@ -363,9 +381,9 @@ __global__ __launch_bounds__(256) void qmm_typed_mfma_kernel(const void* x, cons
   }
   // output element (row 4 (lane >> 4) + e, column lane & 15) of each 16 x 16 tile
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FT; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + wm + 16 * i + 4 * (lane >> 4) + e, n = n0 + wn + 16 * j + (lane & 15);
@@ -400,19 +418,19 @@ typed_mv_fn pick_mv_lds(int dtype, int bits, int gs) {
   return nullptr;
 }
 
-template <int DT, int BITS>
+template <int DT, int BITS, int TB>
 typed_fn pick_mfma_gs(int gs) {
-  if (gs == 32) return qmm_typed_mfma_kernel<DT, BITS, 32>;
-  if (gs == 64) return qmm_typed_mfma_kernel<DT, BITS, 64>;
-  if (gs == 128) return qmm_typed_mfma_kernel<DT, BITS, 128>;
+  if (gs == 32) return qmm_typed_mfma_kernel<DT, BITS, 32, TB>;
+  if (gs == 64) return qmm_typed_mfma_kernel<DT, BITS, 64, TB>;
+  if (gs == 128) return qmm_typed_mfma_kernel<DT, BITS, 128, TB>;
   return nullptr;
 }
 
-template <int DT>
+template <int DT, int TB>
 typed_fn pick_mfma(int bits, int gs) {
-  if (bits == 2) return pick_mfma_gs<DT, 2>(gs);
-  if (bits == 4) return pick_mfma_gs<DT, 4>(gs);
-  if (bits == 8) return pick_mfma_gs<DT, 8>(gs);
+  if (bits == 2) return pick_mfma_gs<DT, 2, TB>(gs);
+  if (bits == 4) return pick_mfma_gs<DT, 4, TB>(gs);
+  if (bits == 8) return pick_mfma_gs<DT, 8, TB>(gs);
   return nullptr;
 }
 
@@ -445,10 +463,15 @@ typed_fn pick(int dtype, int bits, int gs) {
 int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* w, const void* s, const void* b,
                     void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype) {
   typed_fn fn = matvec ? pick<true>(dtype, bits, gs) : pick<false>(dtype, bits, gs);
-  // 16-bit compute dtypes: the matrix-core matmul (x 16-byte aligned)
-  if (!matvec && fn && reinterpret_cast<uintptr_t>(x) % 16 == 0 && tune_int("LISAQ_TYPED_MFMA", 1) != 0) {
-    if (dtype == LISAQ_DTYPE_BF16) fn = pick_mfma<0>(bits, gs);
-    else if (dtype == LISAQ_DTYPE_F16) fn = pick_mfma<2>(bits, gs);
+  // 16-bit compute dtypes: the matrix-core matmul (x 16-byte aligned), in
+  // 128 x 128 tiles where those still make at least 256 workgroups
+  int tile = 64;
+  if (!matvec && fn && reinterpret_cast<uintptr_t>(x) % 16 == 0 && tune_int("LISAQ_TYPED_MFMA", 1) != 0 &&
+      (dtype == LISAQ_DTYPE_BF16 || dtype == LISAQ_DTYPE_F16)) {
+    const bool wide = ((M + 127) / 128) * ((N + 127) / 128) >= 256 && tune_int("LISAQ_TYPED_TB", 2) == 2;
+    if (dtype == LISAQ_DTYPE_BF16) fn = wide ? pick_mfma<0, 2>(bits, gs) : pick_mfma<0, 1>(bits, gs);
+    else fn = wide ? pick_mfma<2, 2>(bits, gs) : pick_mfma<2, 1>(bits, gs);
+    if (wide) tile = 128;
   }
   if (!fn) return set_error(LISAQ_EUNSUPPORTED, "quantized_matmul_typed: dtype=%d bits=%d gs=%d", dtype, bits, gs);
   // grid.y carries the 64-row tiles of M (at most 65535 of them)
@@ -478,8 +501,8 @@ int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* 
   if (matvec)
     hipLaunchKernelGGL(fn, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, w, s, b, y, (int)M, (int)N, (int)K);
   else
-    hipLaunchKernelGGL(fn, dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64)), dim3(256), 0, st, x, w, s,
-                       b, y, (int)M, (int)N, (int)K);
+    hipLaunchKernelGGL(fn, dim3((unsigned)((N + tile - 1) / tile), (unsigned)((M + tile - 1) / tile)), dim3(256), 0,
+                       st, x, w, s, b, y, (int)M, (int)N, (int)K);
   return check_launch("quantized_matmul_typed");
 }
 

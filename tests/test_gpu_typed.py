@@ -97,3 +97,22 @@ def test_quantized_matmul_typed_long_k(dev, oracle, dtype, M):
         ref = oracle.qmm_typed(xf, w, sf, bf, gs, bits, dtype)
     _close(got, ref, dtype, f"{dtype} K={K} M={M}")
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype,bits", [("f16", 4), ("bf16", 8), ("f16", 2)])
+def test_quantized_matmul_typed_wide_tiles(dev, oracle, dtype, bits):
+    """M, N ragged and large enough for the matrix-core matmul's 128 x 128 tiles (at least 256 of
+    them: 16 x 17 here), against the oracle's matmul semantics."""
+    import torch
+
+    rng = np.random.default_rng(2000 + bits)
+    M, N, K, gs = 2000, 2100, 256, 64
+    w, s, b = np_linear(rng, N, K, bits, gs, s_std=0.02 if bits < 8 else 0.002)
+    sf = oracle._round_to(bf16_bits_to_f32(s), dtype)
+    bf = oracle._round_to(bf16_bits_to_f32(b), dtype)
+    xf = oracle._round_to(rng.standard_normal((M, K)).astype(np.float32), dtype)
+    y = ops._mm_typed(_tensor(xf, dtype, dev), to_dev_u32(w, dev), _tensor(sf, dtype, dev), _tensor(bf, dtype, dev),
+                      True, gs, bits, _tensor(xf[:1], dtype, dev).dtype)
+    got = y.float().cpu().numpy()
+    _close(got, oracle.qmm_typed(xf, w, sf, bf, gs, bits, dtype), dtype, f"{dtype} bits={bits} wide tiles")
+    torch.cuda.synchronize()
