@@ -200,6 +200,97 @@ __global__ __launch_bounds__(256) void qmv_typed_lds_kernel(const void* x, const
   }
 }
 
+// f16 with 4-bit codes: the matvec on dot instructions.  A code q becomes
+// the f16 128 + q exactly (bits 0x5800 | q << 3), so one word of 8 codes
+// gives the pairs (128 + q_j, 128 + q_{j+4}) with one shift, one mask and one
+// shift-or, and v_dot2_f32_f16 takes each against the pair (x_j, x_{j+4}) of
+// f16 x (products exact in f32, f32 accumulation).  Per 32-code chunk:
+// y += s * (acc - 128 sum(x)) + b * sum(x), sum(x) of the chunk in f32 once
+// per workgroup.  Up to four rows of x staged in LDS as those pairs, with the
+// chunk sums beside; rows of W walked with a grid stride.  The summation
+// order differs from the plain kernel's (within the output tolerance).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <int GS>
+__global__ __launch_bounds__(256) void qmv_f16_dot_kernel(const void* x, const uint32_t* w, const void* s,
+                                                          const void* b, void* y, int M, int N, int K, int MB) {
+  constexpr int MBX = 4;
+  extern __shared__ __attribute__((aligned(16))) unsigned char xsm[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int C = K / 32, G = K / GS;
+  const int64_t wstride = K / 8;  // u32 words per row
+  uint32_t* xp = reinterpret_cast<uint32_t*>(xsm);                          // [MB][K / 2] pairs
+  float* xsum = reinterpret_cast<float*>(xsm + (size_t)MB * K * 2);         // [MB][C]
+  for (int m0 = 0; m0 < M; m0 += MB) {
+    const int mb = M - m0 < MB ? M - m0 : MB;
+    __syncthreads();  // (the previous group's reads are done)
+    {
+      // each thread: 8 values of x -> the pairs (x0,x4), (x1,x5), (x2,x6), (x3,x7)
+      const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(x) + (int64_t)m0 * K);
+      const int nblk = mb * K / 8;
+      for (int i = tid; i < nblk; i += 256) {
+        const u32x4 v = src[i];
+        u32x4 o;
+        o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+        o[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+        o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+        o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+        reinterpret_cast<u32x4*>(xp)[i] = o;
+      }
+      // chunk sums of x in f32, in index order
+      const uint16_t* xh = static_cast<const uint16_t*>(x) + (int64_t)m0 * K;
+      for (int i = tid; i < mb * C; i += 256) {
+        float t = 0.f;
+        for (int j = 0; j < 32; ++j) t += (float)__builtin_bit_cast(_Float16, xh[(int64_t)i * 32 + j]);
+        xsum[i] = t;
+      }
+    }
+    __syncthreads();
+    for (int n = blockIdx.x * 4 + wave; n < N; n += gridDim.x * 4) {  // (wave-uniform)
+      const uint32_t* wrow = w + (int64_t)n * wstride;
+      float part[MBX];
+#pragma unroll
+      for (int r = 0; r < MBX; ++r) part[r] = 0.f;
+      for (int c = lane; c < C; c += 64) {
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(wrow + c * 4);
+        uint32_t wp[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) wp[4 * i + j] = (((wv[i] >> (4 * j)) & 0x000F000Fu) << 3) | 0x58005800u;
+        const int g = c * 32 / GS;
+        const float sc = ld<2>(s, (int64_t)n * G + g), bi = ld<2>(b, (int64_t)n * G + g);
+#pragma unroll
+        for (int r = 0; r < MBX; ++r) {
+          if (r >= mb) break;
+          const u32x4* xr = reinterpret_cast<const u32x4*>(xp + (size_t)r * (K / 2) + c * 16);
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u32x4 xv = xr[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              // (the element copied out first: a bit cast of a vector element
+              // in place read the vector's first element for every j)
+              const uint32_t xw = xv[j];
+              acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, xw), __builtin_bit_cast(f16x2, wp[4 * i + j]), acc,
+                                           false);
+            }
+          }
+          const float xs = xsum[r * C + c];
+          part[r] = fmaf(sc, fmaf(-128.0f, xs, acc), fmaf(bi, xs, part[r]));
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < MBX; ++r) {
+        if (r >= mb) break;
+        const float t = wsum64(part[r]);
+        if (lane == 0) st<2>(y, (int64_t)(m0 + r) * N + n, t);
+      }
+    }
+  }
+}
+
 // Matmul: 64 x 64 output tile per workgroup, K in steps of 32 through LDS (x
 // and the dequantized, T-rounded weights, both as f32), 4 x 4 outputs per
 // thread.
@@ -477,6 +568,28 @@ int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* 
   // grid.y carries the 64-row tiles of M (at most 65535 of them)
   if (!matvec && (M + 63) / 64 > 65535)
     return set_error(LISAQ_EINVAL_SHAPE, "quantized_matmul_typed: M=%lld exceeds %d rows", (long long)M, 65535 * 64);
+  // f16 x with 4-bit codes, two rows of x or more: the dot-instruction matvec
+  // (x, W 16-byte aligned).  Measured (17408 x 5120, graph-replayed; kernel
+  // reading x from global memory -> this one): M=2 33.8 -> 29.0 us, M=4
+  // 56.2 -> 44.7; one row stays on the global-x kernel (22.4 vs 23.4 here,
+  // 7.8 vs 6.8 at 2560 x 9728): its 4352 small workgroups hide the latency
+  // of each row's loads, which this kernel's rows walked in turn do not
+  if (matvec && dtype == LISAQ_DTYPE_F16 && bits == 4 && M >= 2 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(w) % 16 == 0 && tune_int("LISAQ_TYPED_F16_DOT", 1) != 0) {
+    const int64_t per_row = K * 2 + (K / 32) * 4;  // pairs + chunk sums
+    const int64_t mbd = (160 * 1024) / per_row;
+    typed_mv_fn fd = gs == 32 ? qmv_f16_dot_kernel<32> : gs == 64 ? qmv_f16_dot_kernel<64>
+                   : gs == 128 ? qmv_f16_dot_kernel<128> : nullptr;
+    if (fd && mbd >= 1) {
+      const int MB = (int)(mbd < 4 ? mbd : 4) < M ? (int)(mbd < 4 ? mbd : 4) : (int)M;
+      const int lds = (int)(MB * per_row);
+      if (int rc = allow_dyn_lds((const void*)fd, lds, "quantized_matmul_typed")) return rc;
+      const int64_t rows4 = (N + 3) / 4;
+      const unsigned grid = (unsigned)(rows4 < 2048 ? rows4 : 2048);
+      hipLaunchKernelGGL(fd, dim3(grid), dim3(256), lds, st, x, w, s, b, y, (int)M, (int)N, (int)K, MB);
+      return check_launch("quantized_matmul_typed");
+    }
+  }
   // matvec with x staged in LDS (rows of x per group as the LDS allows, at
   // most four; x 16-byte aligned): for f32, and for 16-bit x from four rows
   // on.  Measured (gs 64, graph-replayed; global-x kernel -> this one):

@@ -74,11 +74,11 @@ def test_promotion_bf16_x_f32_scales(dev, oracle):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
-@pytest.mark.parametrize("M", [1, 64])
+@pytest.mark.parametrize("M", [1, 3, 64])
 def test_quantized_matmul_typed_long_k(dev, oracle, dtype, M):
     """K = 5120: the matvec's lanes take several 32-code chunks each (K/32 =
-    160 chunks over 64 lanes) and the matmul's K loop runs 80 steps over 16
-    column tiles."""
+    160 chunks over 64 lanes; f16 with three rows: the dot-instruction
+    matvec) and the matmul's K loop runs 80 steps over 16 column tiles."""
     import torch
 
     rng = np.random.default_rng(5120 + M)
@@ -90,8 +90,8 @@ def test_quantized_matmul_typed_long_k(dev, oracle, dtype, M):
     y = ops.quantized_matmul(_tensor(xf, dtype, dev), to_dev_u32(w, dev), _tensor(sf, dtype, dev),
                              _tensor(bf, dtype, dev), True, gs, bits)
     got = y.float().cpu().numpy()
-    assert (M < ops.qmv_batch_limit(K, N)) == (M == 1)  # both sides of the split
-    if M == 1:
+    assert (M < ops.qmv_batch_limit(K, N)) == (M < 64)  # both sides of the split
+    if M < 64:
         ref = oracle.qmv_typed(xf, w, sf, bf, gs, bits)
     else:
         ref = oracle.qmm_typed(xf, w, sf, bf, gs, bits, dtype)
