@@ -555,11 +555,13 @@ int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* 
                     void* y, int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype) {
   typed_fn fn = matvec ? pick<true>(dtype, bits, gs) : pick<false>(dtype, bits, gs);
   // 16-bit compute dtypes: the matrix-core matmul (x 16-byte aligned), in
-  // 128 x 128 tiles where those still make at least 256 workgroups
+  // 128 x 128 tiles where those make at least 512 workgroups (measured, f16
+  // 4-bit: 512 x 17408 x 5120, 544 tiles, 397 vs 242 TFLOP/s for 64 x 64;
+  // bf16 8-bit 1024 x 4096 x 4096, 256 tiles, 264 vs 331)
   int tile = 64;
   if (!matvec && fn && reinterpret_cast<uintptr_t>(x) % 16 == 0 && tune_int("LISAQ_TYPED_MFMA", 1) != 0 &&
       (dtype == LISAQ_DTYPE_BF16 || dtype == LISAQ_DTYPE_F16)) {
-    const bool wide = ((M + 127) / 128) * ((N + 127) / 128) >= 256 && tune_int("LISAQ_TYPED_TB", 2) == 2;
+    const bool wide = ((M + 127) / 128) * ((N + 127) / 128) >= 512 && tune_int("LISAQ_TYPED_TB", 2) == 2;
     if (dtype == LISAQ_DTYPE_BF16) fn = wide ? pick_mfma<0, 2>(bits, gs) : pick_mfma<0, 1>(bits, gs);
     else fn = wide ? pick_mfma<2, 2>(bits, gs) : pick_mfma<2, 1>(bits, gs);
     if (wide) tile = 128;

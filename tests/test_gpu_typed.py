@@ -101,12 +101,12 @@ def test_quantized_matmul_typed_long_k(dev, oracle, dtype, M):
 
 @pytest.mark.parametrize("dtype,bits", [("f16", 4), ("bf16", 8), ("f16", 2)])
 def test_quantized_matmul_typed_wide_tiles(dev, oracle, dtype, bits):
-    """M, N ragged and large enough for the matrix-core matmul's 128 x 128 tiles (at least 256 of
-    them: 16 x 17 here), against the oracle's matmul semantics."""
+    """M, N ragged and large enough for the matrix-core matmul's 128 x 128 tiles (at least 512 of
+    them: 16 x 33 here), against the oracle's matmul semantics."""
     import torch
 
     rng = np.random.default_rng(2000 + bits)
-    M, N, K, gs = 2000, 2100, 256, 64
+    M, N, K, gs = 2000, 4200, 256, 64
     w, s, b = np_linear(rng, N, K, bits, gs, s_std=0.02 if bits < 8 else 0.002)
     sf = oracle._round_to(bf16_bits_to_f32(s), dtype)
     bf = oracle._round_to(bf16_bits_to_f32(b), dtype)
