@@ -111,8 +111,8 @@ LISAQ_API int lisaq_quantized_matmul(void* stream, const void* x, const uint32_t
  * QM:767-830, 996-1088), larger M the matmul arithmetic (weights rounded to T
  * from an f32 fma, f32 accumulation, QM:585-703, 1208-1326); y rounded to T
  * once.  Those paths use no workspace: the matvec one wave per output row
- * (x staged in LDS for f32 and from four rows on; f16 with 4-bit codes from
- * two rows on through dot instructions), the matmul on the matrix cores for
+ * (x staged in LDS for f32 and from four rows on; f16 with 4-bit codes
+ * through dot instructions), the matmul on the matrix cores for
  * bf16/f16 (64 x 64 or 128 x 128 tiles; x 16-byte aligned, else and for f32
  * 64 x 64 f32-FMA tiles). */
 LISAQ_API int lisaq_quantized_matmul_typed(void* stream, const void* x, const uint32_t* w, const void* scales,

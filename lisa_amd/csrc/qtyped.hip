@@ -291,6 +291,46 @@ __global__ __launch_bounds__(256) void qmv_f16_dot_kernel(const void* x, const u
   }
 }
 
+// f16 with 4-bit codes at one row of x: the same dot-instruction arithmetic
+// with a wave per output row on a grid of all rows (like the kernel reading
+// x from global memory above): each lane reads its chunk's 32 values of x
+// (cached), pairs them, and takes sum(x) of the chunk with dots against (1, 1).
+template <int GS>
+__global__ __launch_bounds__(256) void qmv_f16_dot1_kernel(const void* x, const uint32_t* w, const void* s,
+                                                           const void* b, void* y, int M, int N, int K) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int C = K / 32, G = K / GS;
+  const uint32_t* wrow = w + (int64_t)n * (K / 8);
+  const u32x4* xq = static_cast<const u32x4*>(x);
+  float part = 0.f;
+  for (int c = lane; c < C; c += 64) {
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(wrow + c * 4);
+    const int g = c * 32 / GS;
+    const float sc = ld<2>(s, (int64_t)n * G + g), bi = ld<2>(b, (int64_t)n * G + g);
+    float acc = 0.f, xs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = xq[c * 4 + i];  // values 32 c + 8 i .. + 7
+      uint32_t pr[4];
+      pr[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);  // (x0, x4)
+      pr[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);  // (x1, x5)
+      pr[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);  // (x2, x6)
+      pr[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);  // (x3, x7)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wp = (((wv[i] >> (4 * j)) & 0x000F000Fu) << 3) | 0x58005800u;
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pr[j]), __builtin_bit_cast(f16x2, wp), acc, false);
+        xs = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pr[j]), __builtin_bit_cast(f16x2, 0x3C003C00u), xs, false);
+      }
+    }
+    part = fmaf(sc, fmaf(-128.0f, xs, acc), fmaf(bi, xs, part));
+  }
+  const float t = wsum64(part);
+  if (lane == 0) st<2>(y, n, t);
+}
+
 // Matmul: 64 x 64 output tile per workgroup, K in steps of 32 through LDS (x
 // and the dequantized, T-rounded weights, both as f32), 4 x 4 outputs per
 // thread.
@@ -570,6 +610,16 @@ int launch_typed_mm(hipStream_t st, bool matvec, const void* x, const uint32_t* 
   // grid.y carries the 64-row tiles of M (at most 65535 of them)
   if (!matvec && (M + 63) / 64 > 65535)
     return set_error(LISAQ_EINVAL_SHAPE, "quantized_matmul_typed: M=%lld exceeds %d rows", (long long)M, 65535 * 64);
+  // f16 x with 4-bit codes at one row: the one-row dot kernel (x, W 16-byte aligned)
+  if (matvec && dtype == LISAQ_DTYPE_F16 && bits == 4 && M == 1 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(w) % 16 == 0 && tune_int("LISAQ_TYPED_F16_DOT1", 1) != 0) {
+    typed_fn f1 = gs == 32 ? qmv_f16_dot1_kernel<32> : gs == 64 ? qmv_f16_dot1_kernel<64>
+                : gs == 128 ? qmv_f16_dot1_kernel<128> : nullptr;
+    if (f1) {
+      hipLaunchKernelGGL(f1, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, w, s, b, y, (int)M, (int)N, (int)K);
+      return check_launch("quantized_matmul_typed");
+    }
+  }
   // f16 x with 4-bit codes, two rows of x or more: the dot-instruction matvec
   // (x, W 16-byte aligned).  Measured (17408 x 5120, graph-replayed; kernel
   // reading x from global memory -> this one): M=2 33.8 -> 29.0 us, M=4
